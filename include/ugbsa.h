@@ -1,0 +1,110 @@
+/* libugbsa — C ABI of the MI355X (gfx950) sparse-prefill hot path.
+ *
+ * The reference implements this path as Python/torch + Triton inside
+ * src/sparse_attention.py (_block_select_kv_idx_v2, :588-748) and
+ * src/triton_block_attn.py (block_sparse_attn_v2, :267-298, kernel :184-264).
+ * Each entry point below replaces one of those pieces; the Python host layer
+ * (sparse_attention.py / block_attn.py in the package) calls them through
+ * ctypes with torch-owned device pointers.
+ *
+ * Conventions
+ *  - Pointers are device pointers (e.g. torch.Tensor.data_ptr()); the library
+ *    never allocates or frees device memory and keeps no pointer after return.
+ *  - Strides are in elements (int64).  bf16 operands need head_dim stride 1,
+ *    16-byte aligned base pointers and other strides that are multiples of 8.
+ *  - Every launch is asynchronous on `stream` (a hipStream_t; NULL = default
+ *    stream).  No entry point synchronises the host.
+ *  - Return value: 0 on success, > 0 a hipError_t from the launch, < 0 an
+ *    argument error (UGBSA_E*).  ugbsa_last_error() gives a message for the
+ *    calling thread's last failure.
+ *  - Key blocks are 64 tokens (the reference's BLOCK, src/sparse_attention.py:51).
+ */
+#ifndef UGBSA_H
+#define UGBSA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UGBSA_ABI_VERSION 1
+
+#define UGBSA_OK 0
+#define UGBSA_EARG (-1)     /* bad size / value / null pointer */
+#define UGBSA_ELAYOUT (-2)  /* stride or alignment the kernels cannot read */
+#define UGBSA_EDTYPE (-3)   /* unsupported element type */
+
+#define UGBSA_DTYPE_BF16 0
+
+#define UGBSA_MODE_MEAN 0   /* K-mean backbone (Selector.router_score "mean", mode "topk") */
+#define UGBSA_MODE_QUEST 1  /* Quest K-max/K-min backbone (mode "quest", router_score "quest") */
+
+#define UGBSA_GRAIN_CELL 0  /* Selector.router_grain */
+#define UGBSA_GRAIN_ROW 1
+#define UGBSA_ROUTER_ABS 0  /* Selector.router_mode */
+#define UGBSA_ROUTER_QUANTILE 1
+
+int ugbsa_abi_version(void);
+const char* ugbsa_last_error(void);
+
+/* Number of bf16 elements of the block-summary buffer [B, Hk, NB, P, D]
+ * (P = 2 for Quest, 3 for mean). */
+int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode);
+
+/* Kernel 1 — per-64-token-block K summaries of k [B, Hk, N, D] bf16.
+ * Replaces the summary step of _block_select_kv_idx_v2:
+ * src/sparse_attention.py:618-622 (zero pad), :636-637 (amin/amax, Quest),
+ * :646 (mean).  Output planes: Quest (K-max, K-min), mean (hi, mid, lo bf16
+ * terms of the fp32 mean). */
+int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                        int B, int Hk, int N, int D, int dtype, int mode, void* planes,
+                        void* stream);
+
+/* Kernel 2 — fused per-Q-tile block scoring, tile max-pool, visibility,
+ * sink/self forcing, top-k_slots and (if sigma != NULL) the sigma margin.
+ * Replaces src/sparse_attention.py:623-707 of _block_select_kv_idx_v2
+ * (per-row scores :638-648, tile max :655-656, causal tile mask :660-666,
+ * FMAX forcing :675-681, topk :697, margin :703-707).
+ * q [B, H, M, D] bf16 (query head h uses KV head h / (H / Hk));
+ * kv_idx out [B, H, Qt, k_slots] int32 contiguous, slots ordered by
+ * (score desc, block asc); sigma out [B, H, Qt] fp32; tile_score (optional
+ * diagnostic) out [B, H, Qt, NB] fp32 = the exact scores ranked.
+ * Qt = ceil(M / 64), NB = ceil(N / 64); block_m must be 64. */
+int ugbsa_select(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                 const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                 int mode, float scaling, int k_base, int k_slots, int block_m, int32_t* kv_idx,
+                 float* sigma, float* tile_score, void* stream);
+
+/* Router — row/cell grain, quantile/abs trigger and sentinel emission.
+ * Replaces src/sparse_attention.py:708-725.  k_quant = max(1, int(q * B*H*Qt))
+ * computed by the caller as the reference does (:714).  Writes sigma_eff
+ * [B, H, Qt] fp32 (after the head mean for row grain), uncertain [B, H, Qt]
+ * uint8, the threshold (1 float, optional) and sets kv_idx[..., k_base:] = NB
+ * for tiles that are not uncertain. */
+int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode, float tau,
+                 int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots, int NB,
+                 float* sigma_eff, uint8_t* uncertain, float* threshold, void* stream);
+
+/* Number of bf16 elements of the attention workspace (V transposed per block). */
+int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D);
+
+/* Kernel 3 — block-sparse causal attention over kv_idx.
+ * Replaces block_sparse_attn_v2 (src/triton_block_attn.py:267-298) and its
+ * kernel _fwd_kernel_v2 (:184-264).  q [B, H, M, D], k/v [B, Hk, N, D] bf16
+ * (Hk may equal H, as after repeat_kv), kv_idx [B, H, Qt, k_slots] int32 with
+ * Qt = ceil(M / block_m), block_m 64 or 32, sentinel NB skipped; out
+ * [B, H, M, D] bf16 with arbitrary strides (head_dim stride 1). */
+int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                   const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                   const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                   const int32_t* kv_idx, int64_t si_b, int64_t si_h, int64_t si_t,
+                   int64_t si_s, int B, int H, int Hk, int M, int N, int D, int dtype, int Qt,
+                   int k_slots, int block_m, float scale, void* out, int64_t so_b,
+                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UGBSA_H */

@@ -42,8 +42,11 @@ def visited_blocks(row, t: int, n_blocks: int, block_m: int = 64, block_n: int =
 
 
 def gathered_attention(q, k, v, kv_idx, scale: float, block_m: int = 64,
-                       block_n: int = 64):
-    """[B, H, M, D] fp32 output of the v2 kernel semantics."""
+                       block_n: int = 64, tiles=None, heads=None):
+    """[B, H, M, D] fp32 output of the v2 kernel semantics.
+
+    ``tiles`` / ``heads`` restrict the work to a subset (rows outside stay 0).
+    """
     q, k, v = _f32(q), _f32(k), _f32(v)
     kv = np.asarray(kv_idx)
     B, H, M, D = q.shape
@@ -52,10 +55,12 @@ def gathered_attention(q, k, v, kv_idx, scale: float, block_m: int = 64,
     nb = (N + block_n - 1) // block_n
     out = np.zeros((B, H, M, D), np.float32)
     sc = np.float32(scale)
+    tiles = range(kv.shape[2]) if tiles is None else tiles
+    heads = range(H) if heads is None else heads
     for b in range(B):
-        for h in range(H):
+        for h in heads:
             kh = h // grp
-            for t in range(kv.shape[2]):
+            for t in tiles:
                 r0 = t * block_m
                 if r0 >= M:
                     continue

@@ -163,7 +163,7 @@ def main():
     small_case(sa, "a", S=1024, Hq=4, Hkv=2, D=64, needles=4, budget=2, k_min=1,
                seed_layer=11, quantile=0.25)
     # B: ragged — S not a multiple of 64 (padded last block and last tile).
-    small_case(sa, "b_ragged", S=1000, Hq=2, Hkv=1, D=32, needles=3, budget=2, k_min=1,
+    small_case(sa, "b_ragged", S=1000, Hq=2, Hkv=1, D=64, needles=3, budget=2, k_min=1,
                seed_layer=12, quantile=0.25)
     # C: k_base = NB/2 so k_slots = NB exactly (NB = 8).
     small_case(sa, "c_full", S=512, Hq=4, Hkv=1, D=64, needles=2, budget=2, k_min=1,

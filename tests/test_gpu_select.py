@@ -1,0 +1,222 @@
+"""GPU parity of kernels 1, 2 and the router against the CPU oracle.
+
+Bars:
+* block summaries — Quest planes bit-exact (min/max of bf16 with F.pad zeros);
+  mean planes hi+mid+lo within 2 fp32 ulps of the oracle's fp32 mean;
+* selection on the kernel's own fp32 tile scores — kv_idx, sigma, sigma_eff,
+  trigger flags and threshold bit-identical to the oracle run on those scores;
+* kernel scores vs oracle scores from the same bf16 inputs — max |dT| <= 1e-5;
+* kv_idx vs the oracle from scratch and vs the reference's golden vectors —
+  equal except rows explained by near ties (tests/parity.py).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import _capi
+import sparse_attention as sa
+import synth
+from conftest import load_golden
+from oracle import selector as OS
+from parity import f32np, same_float_bits, unexplained_differences
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def make_sel(**fields):
+    s = sa.Selector()
+    s.kernel_v2 = True
+    for k, v in fields.items():
+        setattr(s, k, v)
+    return s
+
+
+def run_summary(k, mode):
+    lib = _capi.lib()
+    B, Hk, N, D = k.shape
+    planes = torch.empty(lib.ugbsa_summary_elems(B, Hk, N, D, mode), dtype=torch.bfloat16, device=DEV)
+    _capi.check(lib.ugbsa_block_summary(k.data_ptr(), *k.stride(), B, Hk, N, D, _capi.DTYPE_BF16,
+                                        mode, planes.data_ptr(), _capi.stream_ptr(DEV)), "summary")
+    torch.cuda.synchronize()
+    nb = (N + 63) // 64
+    return planes.view(B, Hk, nb, 2 if mode == _capi.MODE_QUEST else 3, D)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_block_summary(hip_lib, D):
+    print(f"[case] block_summary D={D}", flush=True)
+    g = torch.Generator().manual_seed(D)
+    k = torch.randn(2, 3, 1000, D, generator=g).to(torch.bfloat16)      # ragged last block
+    kd = k.to(DEV)
+    kmin, kmax = OS.block_summaries(k.float().numpy(), True)
+    kmean = OS.block_summaries(k.float().numpy(), False)
+    pq = run_summary(kd, _capi.MODE_QUEST).float().cpu().numpy()
+    assert np.array_equal(pq[..., 0, :], kmax) and np.array_equal(pq[..., 1, :], kmin)
+    pm = run_summary(kd, _capi.MODE_MEAN).float().cpu().numpy().astype(np.float64)
+    mean3 = pm[..., 0, :] + pm[..., 1, :] + pm[..., 2, :]
+    # both fp32 means (kernel: sequential sums; oracle: numpy pairwise) sit within
+    # the fp32 summation bound 64 * 2^-24 * mean|x| of the exact mean
+    kp = np.zeros((2, 3, 1024, D))
+    kp[:, :, :1000] = k.double().numpy()
+    blocks = kp.reshape(2, 3, 16, 64, D)
+    exact = blocks.mean(axis=3)
+    bound = 64 * 2.0 ** -24 * np.abs(blocks).mean(axis=3) + 1e-30
+    assert (np.abs(mean3 - exact) <= bound).all()
+    assert (np.abs(kmean - exact) <= bound).all()
+
+
+POLICIES = {
+    "topk": dict(mode="topk"),
+    "quest": dict(mode="quest"),
+    "router_quest_row_q": dict(mode="router", router_score="quest", router_grain="row",
+                               router_mode="quantile", router_quantile=0.25),
+    "router_mean_row_q": dict(mode="router", router_score="mean", router_grain="row",
+                              router_mode="quantile", router_quantile=0.25),
+    "router_quest_cell_q": dict(mode="router", router_score="quest", router_grain="cell",
+                                router_mode="quantile", router_quantile=0.25),
+    "router_mean_cell_abs": dict(mode="router", router_score="mean", router_grain="cell",
+                                 router_mode="abs"),
+    "router_quest_row_q090": dict(mode="router", router_score="quest", router_grain="row",
+                                  router_mode="quantile", router_quantile=0.90),
+}
+
+
+def gpu_vs_oracle_on_kernel_scores(q, k, scaling, sel):
+    res = sa.select_v2(q.to(DEV), k.to(DEV), scaling, sel=sel, want_tile_score=True)
+    torch.cuda.synchronize()
+    T = res.tile_score.cpu().numpy()
+    ocfg = OS.SelectorConfig.from_selector(sel)
+    o = OS.select_from_tile_scores(T, ocfg)
+    assert np.array_equal(res.kv_idx.cpu().numpy(), o.kv_idx), "kv_idx differs on the same scores"
+    if o.sigma is not None:
+        assert same_float_bits(res.sigma.cpu().numpy(), o.sigma), "sigma bits"
+        assert same_float_bits(res.sigma_eff.cpu().numpy(), o.sigma_eff), "sigma_eff bits"
+        assert np.array_equal(res.uncertain.cpu().numpy().astype(bool), o.uncertain)
+        if o.threshold is not None:
+            thr = res.threshold.cpu().numpy()[0]
+            assert (np.isnan(thr) and np.isnan(o.threshold)) or same_float_bits(thr, o.threshold)
+    return res, o
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("policy", sorted(POLICIES))
+def test_select_exact_on_kernel_scores(hip_lib, D, policy):
+    print(f"[case] select D={D} policy={policy}", flush=True)
+    cfg = synth.CONFIGS["c1"]
+    S = 2000 if D != 128 else 4096                       # ragged and aligned
+    q, k, _ = synth.make_layer(cfg, 3, S=S, D=D, dtype=torch.bfloat16)
+    sel = make_sel(budget_blocks=4, k_min=1, **POLICIES[policy])
+    res, o = gpu_vs_oracle_on_kernel_scores(q, k, D ** -0.5, sel)
+    # scores agree with the oracle's independent fp32 scores
+    T_or = OS.tile_scores(q.float().numpy(), k.float().numpy(), D ** -0.5,
+                          OS.SelectorConfig.from_selector(sel).use_quest)
+    T_k = res.tile_score.cpu().numpy()
+    fin = np.isfinite(T_or)
+    assert np.array_equal(fin, np.isfinite(T_k))
+    assert np.abs(T_or[fin] - T_k[fin]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("name", ["a", "b_ragged", "c_full"])
+def test_select_vs_reference_golden(hip_lib, name):
+    """The reference's own kv_idx (fp32 CPU run) reproduced on the GPU."""
+    print(f"[case] golden {name}", flush=True)
+    inp, pols = load_golden(name)
+    q = torch.from_numpy(inp["q"]).to(torch.bfloat16)   # exact: inputs are bf16 values
+    k = torch.from_numpy(inp["k"]).to(torch.bfloat16)
+    for pol, rec in pols.items():
+        fields = {f: v for f, v in rec["fields"].items()}
+        sel = make_sel(**fields)
+        res, o = gpu_vs_oracle_on_kernel_scores(q, k, float(inp["scaling"]), sel)
+        T_ref = rec["tile_score"]
+        fin = np.isfinite(T_ref)
+        assert np.abs(T_ref[fin] - res.tile_score.cpu().numpy()[fin]).max() <= 1e-5, pol
+        ref = OS.select_from_tile_scores(T_ref, OS.SelectorConfig.from_selector(sel))
+        n_diff, bad = unexplained_differences(
+            res.kv_idx.cpu().numpy(), rec["kv_idx"], T_ref, ref.k_base, ref.k_slots,
+            trig_a=None if res.uncertain is None else res.uncertain.cpu().numpy(),
+            trig_b=ref.uncertain,
+            sig_a=None if res.sigma_eff is None else res.sigma_eff.cpu().numpy(),
+            sig_b=ref.sigma_eff,
+            thr_a=None if res.threshold is None else res.threshold.cpu().numpy()[0],
+            thr_b=ref.threshold)
+        assert not bad, f"{pol}: {len(bad)} unexplained rows of {n_diff} differing"
+
+
+def test_select_c1_full_config(hip_lib):
+    """BASELINE configs[0] layer (S=8192, 8/2 heads, D=128) in bf16 on the GPU."""
+    print("[case] select c1 full", flush=True)
+    cfg = synth.CONFIGS["c1"]
+    q, k, _ = synth.make_layer(cfg, 0, dtype=torch.bfloat16)
+    sel = make_sel(**cfg.sel_fields())
+    res, o = gpu_vs_oracle_on_kernel_scores(q, k, cfg.scaling, sel)
+    assert res.kv_idx.shape == (1, 8, 128, 32)
+    orc = OS.select_kv_idx_v2(q.float().numpy(), k.float().numpy(), cfg.scaling,
+                              OS.SelectorConfig.from_selector(sel))
+    n_diff, bad = unexplained_differences(
+        res.kv_idx.cpu().numpy(), orc.kv_idx, orc.tile_score, orc.k_base, orc.k_slots,
+        res.uncertain.cpu().numpy(), orc.uncertain, res.sigma_eff.cpu().numpy(),
+        orc.sigma_eff, res.threshold.cpu().numpy()[0], orc.threshold)
+    assert not bad, f"{len(bad)} unexplained rows of {n_diff}"
+    assert float(res.uncertain.float().mean()) == 0.25
+
+
+def test_select_c2_full_config(hip_lib):
+    """BASELINE configs[1] layer: S=32768, 28/4 heads, D=128, router-on-Quest 64 -> 128."""
+    print("[case] select c2 full", flush=True)
+    cfg = synth.CONFIGS["c2"]
+    q, k, _ = synth.make_layer(cfg, 0)
+    sel = make_sel(**cfg.sel_fields())
+    res, o = gpu_vs_oracle_on_kernel_scores(q, k, cfg.scaling, sel)
+    assert res.kv_idx.shape == (1, 28, 512, 128) and (res.k_base, res.k_slots) == (64, 128)
+    # oracle scores from scratch for one KV group (7 query heads)
+    ocfg = OS.SelectorConfig.from_selector(sel)
+    T_or = OS.tile_scores(q[:, :7].float().numpy(), k[:, :1].float().numpy(), cfg.scaling, True)
+    T_k = res.tile_score[:, :7].cpu().numpy()
+    fin = np.isfinite(T_or)
+    assert np.abs(T_or[fin] - T_k[fin]).max() <= 1e-5
+    # trigger fraction: kq = int(0.25 * 28 * 512) = 3584 -> 128 tiles of 448 eligible
+    trig_tiles = res.uncertain[0, 0].cpu().numpy().astype(bool)
+    assert trig_tiles.sum() >= 128 and not trig_tiles[:64].any()
+
+
+def test_router_kernel_edge_cases(hip_lib):
+    """Row/cell grain, NaN threshold, abs mode on hand-built sigma arrays."""
+    print("[case] router edges", flush=True)
+    lib = _capi.lib()
+    rng = np.random.default_rng(0)
+    B, H, Qt, kb, ks, nb = 2, 3, 40, 4, 8, 64
+    for grain in (_capi.GRAIN_ROW, _capi.GRAIN_CELL):
+        for rmode, qfrac in ((_capi.ROUTER_QUANTILE, 0.3), (_capi.ROUTER_QUANTILE, 0.99),
+                             (_capi.ROUTER_ABS, 0.0)):
+            sig = (rng.integers(0, 50, (B, H, Qt)) * OS.sigma_quantum()).astype(np.float32)
+            sig[:, :, :5] = np.nan
+            kv = np.tile(np.arange(ks, dtype=np.int32), (B, H, Qt, 1))
+            tau = 20 * OS.sigma_quantum()
+            sd = torch.from_numpy(sig).to(DEV)
+            kvd = torch.from_numpy(kv).to(DEV)
+            eff = torch.empty_like(sd)
+            unc = torch.empty(sd.shape, dtype=torch.uint8, device=DEV)
+            thr = torch.empty(1, device=DEV)
+            kq = max(1, int(qfrac * sig.size))
+            _capi.check(lib.ugbsa_router(sd.data_ptr(), B, H, Qt, grain, rmode, tau, kq,
+                                         kvd.data_ptr(), kb, ks, nb, eff.data_ptr(),
+                                         unc.data_ptr(), thr.data_ptr(), _capi.stream_ptr(DEV)),
+                        "router")
+            torch.cuda.synchronize()
+            want_eff = OS.head_mean(sig) if grain == _capi.GRAIN_ROW else sig
+            assert same_float_bits(eff.cpu().numpy(), want_eff)
+            if rmode == _capi.ROUTER_QUANTILE:
+                want_thr = OS.kth_smallest(want_eff, kq)
+                got = thr.cpu().numpy()[0]
+                assert (np.isnan(want_thr) and np.isnan(got)) or got == want_thr
+                with np.errstate(invalid="ignore"):
+                    want_unc = want_eff <= want_thr
+            else:
+                with np.errstate(invalid="ignore"):
+                    want_unc = want_eff < np.float32(tau)
+            assert np.array_equal(unc.cpu().numpy().astype(bool), want_unc)
+            want_kv = kv.copy()
+            want_kv[..., kb:][~want_unc] = nb
+            assert np.array_equal(kvd.cpu().numpy(), want_kv)

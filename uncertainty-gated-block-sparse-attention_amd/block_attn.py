@@ -1,0 +1,114 @@
+"""Block-sparse attention launchers — the MI355X counterpart of the reference's
+``src/triton_block_attn.py`` (same function names, arguments and asserts).
+
+``block_sparse_attn_v2`` (reference ``:267-298``) launches the gfx950 HIP
+kernel ``attn_fwd_kernel`` through the C ABI; ``_compute_kv_idx`` (``:125-146``)
+and ``reference_attn`` (``:301-312``) are the torch helpers the reference's
+kernel test uses to build ``kv_idx`` from a keep mask and to form the SDPA
+reference.  Differences from the reference launcher, all additive:
+
+* K/V may carry ``Hk`` heads with ``H % Hk == 0`` (GQA: query head h reads KV
+  head h // (H // Hk), transformers' ``repeat_kv`` mapping), so callers need
+  not materialise ``repeat_kv``; equal head counts behave as in the reference.
+* Q/K/V only need unit stride on head_dim (the reference's dispatcher calls
+  ``.contiguous()``); ``out`` may be any such strided view, which lets the
+  dispatcher write the ``[B, S, H, D]`` layout directly.
+* ``num_warps`` / ``num_stages`` are Triton tuning knobs, accepted and ignored.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+import _capi
+
+
+def _bf16_operand(name, t):
+    assert t.is_cuda, f"{name} must be a HIP device tensor"
+    assert t.dtype == torch.bfloat16, f"{name}: bf16 required, got {t.dtype}"
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
+        t = t.contiguous()
+    return t
+
+
+def attn_workspace(B: int, Hk: int, N: int, D: int, device) -> torch.Tensor:
+    """Workspace of ``ugbsa_attn_fwd`` (V transposed per 64-key block)."""
+    n = _capi.lib().ugbsa_attn_workspace_elems(B, Hk, N, D)
+    return torch.empty(n, dtype=torch.bfloat16, device=device)
+
+
+def block_sparse_attn_v2(q, k, v, kv_idx, scale, block_n=64, block_m=64,
+                         num_warps=4, num_stages=1, out=None, workspace=None):
+    """Per-tile-selection block-sparse causal attention (HIP, bf16 MFMA).
+
+    q : [B, H, M, D] bf16; k, v : [B, Hk, N, D] bf16 (Hk == H or H % Hk == 0)
+    kv_idx : [B, H, ceil(M / block_m), MAX_KEPT] int32, sentinel = NB skipped
+    Returns out [B, H, M, D] (``out`` if given).
+    """
+    assert q.dim() == 4 and k.shape == v.shape and q.shape[0] == k.shape[0] \
+        and q.shape[-1] == k.shape[-1], "q [B,H,M,D], k = v [B,Hk,N,D] expected"
+    assert q.is_cuda and kv_idx.dtype == torch.int32
+    assert block_n == 64, "key blocks are 64 tokens"
+    B, H, M, D = q.shape
+    Hk, N = k.shape[1], k.shape[2]
+    assert H % Hk == 0, "query heads must be a multiple of KV heads"
+    assert kv_idx.dim() == 4 and tuple(kv_idx.shape[:3]) == (B, H, (M + block_m - 1) // block_m)
+    q = _bf16_operand("q", q)
+    k = _bf16_operand("k", k)
+    v = _bf16_operand("v", v)
+    if kv_idx.stride(-1) != 1:
+        kv_idx = kv_idx.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+    if workspace is None:
+        workspace = attn_workspace(B, Hk, N, D, q.device)
+    lib = _capi.lib()
+    rc = lib.ugbsa_attn_fwd(
+        q.data_ptr(), *q.stride(),
+        k.data_ptr(), *k.stride(),
+        v.data_ptr(), *v.stride(),
+        kv_idx.data_ptr(), *kv_idx.stride(),
+        B, H, Hk, M, N, D, _capi.DTYPE_BF16, kv_idx.shape[2], kv_idx.shape[3], block_m,
+        float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(),
+        _capi.stream_ptr(q.device))
+    _capi.check(rc, "block_sparse_attn_v2")
+    return out
+
+
+def _compute_kv_idx(keep, block_m):
+    """keep [B, H, M, NB] bool -> (kv_idx [B, H, Qt, MAX_KEPT] int32 ascending,
+    NB-padded; MAX_KEPT).  Same contract as src/triton_block_attn.py:125-146."""
+    B, H, M, NB = keep.shape
+    q_tiles = (M + block_m - 1) // block_m
+    pad = q_tiles * block_m - M
+    if pad:
+        keep = F.pad(keep, (0, 0, 0, pad))
+    any_keep = keep.reshape(B, H, q_tiles, block_m, NB).any(dim=-2)
+    blocks = torch.arange(NB, device=keep.device, dtype=torch.int32)
+    masked = torch.where(any_keep, blocks.view(1, 1, 1, NB),
+                         torch.full((), NB, device=keep.device, dtype=torch.int32))
+    ordered, _ = masked.sort(dim=-1)
+    max_kept = max(1, int((ordered < NB).sum(dim=-1).max().item()))
+    return ordered[..., :max_kept].contiguous(), max_kept
+
+
+def reference_attn(q, k, v, keep, scale, block_n=64):
+    """SDPA with the materialised keep-and-causal mask (src/triton_block_attn.py:301-312).
+
+    Runs in fp32 math (inputs upcast) so it is a reference, not a competitor.
+    """
+    B, H, M, D = q.shape
+    N = k.shape[-2]
+    NB = keep.shape[-1]
+    if k.shape[1] != H:
+        rep = H // k.shape[1]
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+    kk = (keep.unsqueeze(-1).expand(B, H, M, NB, block_n)
+          .reshape(B, H, M, NB * block_n)[..., :N])
+    causal = (torch.arange(N, device=q.device).view(1, N)
+              <= torch.arange(M, device=q.device).view(M, 1))
+    return F.scaled_dot_product_attention(q.float(), k.float(), v.float(),
+                                          attn_mask=kk & causal, scale=scale)

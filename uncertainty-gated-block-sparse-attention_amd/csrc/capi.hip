@@ -1,0 +1,165 @@
+// extern "C" boundary of libugbsa: argument validation, error reporting,
+// dispatch to the kernel launchers.  Declarations and the reference
+// interfaces each entry point replaces: include/ugbsa.h.
+#include <cstdio>
+#include <cstdarg>
+#include <string>
+
+#include "common.h"
+#include "launch.h"
+#include "../../include/ugbsa.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_result(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_error.clear();
+    return UGBSA_OK;
+  }
+  return fail(static_cast<int>(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks a bf16 [B, H, S, D] operand read with 16-byte vector loads.
+int check_bf16_operand(const char* name, const void* p, int64_t s_b, int64_t s_h, int64_t s_s,
+                       int64_t s_d) {
+  if (p == nullptr) return fail(UGBSA_EARG, "%s is null", name);
+  if (s_d != 1) return fail(UGBSA_ELAYOUT, "%s: innermost (head_dim) stride must be 1, got %lld", name, (long long)s_d);
+  if (!aligned16(p)) return fail(UGBSA_ELAYOUT, "%s: data pointer must be 16-byte aligned", name);
+  if (s_b % 8 || s_h % 8 || s_s % 8)
+    return fail(UGBSA_ELAYOUT, "%s: batch/head/sequence strides must be multiples of 8 elements", name);
+  return UGBSA_OK;
+}
+
+int check_dims(int B, int H, int Hk, int D, int dtype) {
+  if (dtype != UGBSA_DTYPE_BF16) return fail(UGBSA_EDTYPE, "only bf16 tensors are supported (dtype code %d)", dtype);
+  if (B < 1 || H < 1 || Hk < 1) return fail(UGBSA_EARG, "B, H, Hk must be positive");
+  if (H % Hk) return fail(UGBSA_EARG, "query heads (%d) must be a multiple of key heads (%d)", H, Hk);
+  if (D != 64 && D != 128 && D != 256) return fail(UGBSA_EARG, "head_dim %d not supported (64, 128, 256)", D);
+  return UGBSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ugbsa_abi_version(void) { return UGBSA_ABI_VERSION; }
+
+const char* ugbsa_last_error(void) { return g_error.c_str(); }
+
+int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode) {
+  const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  return static_cast<int64_t>(B) * Hk * nb * (mode == UGBSA_MODE_QUEST ? 2 : 3) * D;
+}
+
+int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D) {
+  const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  return static_cast<int64_t>(B) * Hk * nb * ugbsa::kBlock * D;
+}
+
+int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                        int B, int Hk, int N, int D, int dtype, int mode, void* planes,
+                        void* stream) {
+  int rc = check_dims(B, Hk, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("k", k, sk_b, sk_h, sk_n, sk_d))) return rc;
+  if (N < 1) return fail(UGBSA_EARG, "N must be positive");
+  if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
+  if (planes == nullptr) return fail(UGBSA_EARG, "planes is null");
+  return hip_result(ugbsa::launch_block_summary(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, B, Hk, N, D,
+                                                mode, static_cast<uint16_t*>(planes),
+                                                static_cast<hipStream_t>(stream)),
+                    "block_summary");
+}
+
+int ugbsa_select(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                 const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                 int mode, float scaling, int k_base, int k_slots, int block_m, int32_t* kv_idx,
+                 float* sigma, float* tile_score, void* stream) {
+  int rc = check_dims(B, H, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
+  if (M < 1 || N < 1) return fail(UGBSA_EARG, "M and N must be positive");
+  if (block_m != 64) return fail(UGBSA_EARG, "selection tiles are 64 rows (block_m=%d)", block_m);
+  if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
+  if (planes == nullptr || kv_idx == nullptr) return fail(UGBSA_EARG, "planes / kv_idx is null");
+  if (!aligned16(planes)) return fail(UGBSA_ELAYOUT, "planes must be 16-byte aligned");
+  const int nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  if (nb > ugbsa::kMaxBlocksSelect) return fail(UGBSA_EARG, "N=%d gives %d key blocks; the selector holds at most %d", N, nb, ugbsa::kMaxBlocksSelect);
+  if (k_slots < 1 || k_slots > nb || k_slots > ugbsa::kMaxSlots)
+    return fail(UGBSA_EARG, "k_slots=%d out of range [1, min(NB=%d, %d)]", k_slots, nb, ugbsa::kMaxSlots);
+  if (k_base < 1 || k_base > k_slots) return fail(UGBSA_EARG, "k_base=%d out of range [1, k_slots=%d]", k_base, k_slots);
+  if (sigma != nullptr && k_base >= k_slots) return fail(UGBSA_EARG, "sigma needs k_base < k_slots");
+  return hip_result(ugbsa::launch_select(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
+                                         static_cast<const uint16_t*>(planes), B, H, Hk, M, N, D,
+                                         mode, scaling, k_base, k_slots, sigma != nullptr, kv_idx,
+                                         sigma, tile_score, static_cast<hipStream_t>(stream)),
+                    "select");
+}
+
+int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode, float tau,
+                 int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots, int NB,
+                 float* sigma_eff, uint8_t* uncertain, float* threshold, void* stream) {
+  if (sigma == nullptr || kv_idx == nullptr || sigma_eff == nullptr || uncertain == nullptr)
+    return fail(UGBSA_EARG, "sigma / kv_idx / sigma_eff / uncertain is null");
+  if (B < 1 || H < 1 || Qt < 1) return fail(UGBSA_EARG, "B, H, Qt must be positive");
+  if (grain != UGBSA_GRAIN_CELL && grain != UGBSA_GRAIN_ROW) return fail(UGBSA_EARG, "unknown router grain %d", grain);
+  if (rmode != UGBSA_ROUTER_ABS && rmode != UGBSA_ROUTER_QUANTILE) return fail(UGBSA_EARG, "unknown router mode %d", rmode);
+  const int64_t n = static_cast<int64_t>(B) * H * Qt;
+  if (rmode == UGBSA_ROUTER_QUANTILE && (k_quant < 1 || k_quant > n))
+    return fail(UGBSA_EARG, "k_quant=%lld out of range [1, %lld]", (long long)k_quant, (long long)n);
+  if (k_base < 1 || k_base >= k_slots || k_slots > NB)
+    return fail(UGBSA_EARG, "router needs 1 <= k_base < k_slots <= NB (%d, %d, %d)", k_base, k_slots, NB);
+  return hip_result(ugbsa::launch_router(sigma, B, H, Qt, grain, rmode, tau, k_quant, kv_idx, k_base,
+                                         k_slots, NB, sigma_eff, uncertain, threshold,
+                                         static_cast<hipStream_t>(stream)),
+                    "router");
+}
+
+int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                   const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                   const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                   const int32_t* kv_idx, int64_t si_b, int64_t si_h, int64_t si_t,
+                   int64_t si_s, int B, int H, int Hk, int M, int N, int D, int dtype, int Qt,
+                   int k_slots, int block_m, float scale, void* out, int64_t so_b,
+                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace, void* stream) {
+  int rc = check_dims(B, H, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
+  if ((rc = check_bf16_operand("k", k, sk_b, sk_h, sk_n, sk_d))) return rc;
+  if ((rc = check_bf16_operand("v", v, sv_b, sv_h, sv_n, sv_d))) return rc;
+  if (out == nullptr) return fail(UGBSA_EARG, "out is null");
+  if (so_d != 1 || (reinterpret_cast<uintptr_t>(out) & 7u) || so_b % 4 || so_h % 4 || so_m % 4)
+    return fail(UGBSA_ELAYOUT, "out: head_dim stride 1, 8-byte aligned rows required");
+  if (kv_idx == nullptr || si_s != 1) return fail(UGBSA_ELAYOUT, "kv_idx must be non-null with unit slot stride");
+  if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace (V block transpose) must be a 16-byte aligned buffer");
+  if (M < 1 || N < 1) return fail(UGBSA_EARG, "M and N must be positive");
+  if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
+  if (Qt != (M + block_m - 1) / block_m) return fail(UGBSA_EARG, "kv_idx holds %d tiles, M=%d needs %d", Qt, M, (M + block_m - 1) / block_m);
+  if (k_slots < 1) return fail(UGBSA_EARG, "k_slots must be positive");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint16_t* vt = static_cast<uint16_t*>(workspace);
+  hipError_t e = ugbsa::launch_v_block_transpose(static_cast<const uint16_t*>(v), sv_b, sv_h, sv_n, B, Hk, N, D, vt, st);
+  if (e != hipSuccess) return hip_result(e, "v_block_transpose");
+  return hip_result(ugbsa::launch_attn_fwd(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
+                                           static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, vt,
+                                           kv_idx, si_b, si_h, si_t, B, H, Hk, M, N, D, Qt,
+                                           k_slots, block_m, scale, static_cast<uint16_t*>(out),
+                                           so_b, so_h, so_m, st),
+                    "attn_fwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,105 @@
+// Shared device helpers for the gfx950 (CDNA4) sparse-prefill kernels.
+//
+// Conventions used by every kernel in this library:
+//  * a wavefront is 64 lanes; lane = 16 * g4 + r16 (g4 = lane >> 4, r16 = lane & 15);
+//  * MFMA v_mfma_f32_16x16x32_bf16: lane (r16, g4) supplies row r16 of A and
+//    column r16 of B, each with 8 consecutive bf16 of the 32-long contraction
+//    (slots 8*g4 .. 8*g4+7); it receives C[4*g4 + i][r16], i = 0..3.  Any
+//    consistent relabelling of the contraction slots between A and B gives the
+//    same product, which the kernels use to permute keys freely;
+//  * bf16 tensors are read with 16-byte vector loads, so the innermost (D)
+//    stride must be 1 and row strides multiples of 8 elements.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ugbsa {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short i16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+constexpr int kWave = 64;
+constexpr int kBlock = 64;          // tokens per KV block (reference BLOCK)
+constexpr float kFMax = 3.40282346638528859812e+38f;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+__device__ __forceinline__ bf16x8 zero_bf16x8() {
+  i16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+  return __builtin_bit_cast(bf16x8, z);
+}
+
+// max(x, 0) / min(x, 0) of eight bf16 values by sign masking (exact).
+__device__ __forceinline__ bf16x8 bf16_pos(bf16x8 x) {
+  i16x8 v = __builtin_bit_cast(i16x8, x);
+  i16x8 s = v >> 15;                 // all ones where negative
+  return __builtin_bit_cast(bf16x8, v & ~s);
+}
+__device__ __forceinline__ bf16x8 bf16_neg(bf16x8 x) {
+  i16x8 v = __builtin_bit_cast(i16x8, x);
+  i16x8 s = v >> 15;
+  return __builtin_bit_cast(bf16x8, v & s);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (inputs here are finite).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float* f) {
+  i16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = static_cast<short>(f32_to_bf16(f[j]));
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Monotone uint32 key of an fp32 value (larger float -> larger key); NaN is
+// mapped above +inf, matching torch.topk / kthvalue's NaN-is-largest order.
+__device__ __forceinline__ uint32_t float_key(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (x != x) return 0xFFFFFFFFu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+  if (k == 0xFFFFFFFFu) return __uint_as_float(0x7FC00000u);
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __uint_as_float(u);
+}
+
+// Cross-lane helpers within one wavefront.
+__device__ __forceinline__ float shfl_xor_f(float v, int m) {
+  return __shfl_xor(v, m, kWave);
+}
+__device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int m) {
+  return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), m, kWave));
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  uint32_t lo = shfl_xor_u(static_cast<uint32_t>(v), m);
+  uint32_t hi = shfl_xor_u(static_cast<uint32_t>(v >> 32), m);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Order LDS traffic of one wavefront against itself (no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace ugbsa

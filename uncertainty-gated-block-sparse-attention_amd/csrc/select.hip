@@ -1,0 +1,371 @@
+// Kernel 2: fused block scoring + tile max-pool + top-k + sigma margin.
+//
+// Restates src/sparse_attention.py:623-707 of the reference without ever
+// materialising the per-row score tensor [B, H, M, NB]:
+//   per-row score   S[r, blk] = sum_p sum_d Qcat_p[r, d] * planes[blk, p, d] * scaling
+//                   (Quest: Qcat = (max(q,0), min(q,0)), planes = (Kmax, Kmin) —
+//                   the two-matmul form of :638-642; mean: Qcat = (q, q, q),
+//                   planes = hi/mid/lo of the fp32 block mean, :647-648);
+//   tile max        T[t, blk] = max over the 64 rows of tile t (:655-656; rows
+//                   past M are zero queries, as the reference's F.pad);
+//   visibility      blocks past the tile's last row are -inf (:660-666);
+//   forcing         T[0] = T[self] = FLT_MAX (:675-681);
+//   top-k           k_slots best blocks ordered by (score desc, block asc) —
+//                   torch.topk with its unspecified tie order made total (:697);
+//   sigma           (s[k_base-1] - s[k_base]) / max(s[0] - s[k_base], 1e-6) in
+//                   IEEE fp32 (correctly rounded division, denormals kept) (:703-707).
+//
+// Workgroup = one (b, KV head g, Q tile t) and up to 8 of the group's query
+// heads, one wavefront per head.  All waves share each 32-block chunk of the
+// KV head's summary planes, staged once in LDS; each wave computes its
+// 64 x 32 score chunk on MFMA (A = its Q tile from registers, B = planes from
+// LDS), max-pools it over rows in registers and appends 32 tile scores to
+// its LDS row.  The row then goes through a 4-pass 8-bit radix select for
+// the k_slots-th best key, a ballot compaction of the winners (ties at the
+// cut taken in block order) and a register bitonic sort.
+#include "common.h"
+#include "launch.h"
+
+namespace ugbsa {
+
+constexpr int kChunk = 32;   // KV blocks per LDS chunk
+
+struct SelectLds {
+  int row_stride;      // elements per chunk row (P * D + 8 pad)
+  int chunk_bytes;
+  int wave_bytes;
+  int trow_off, hist_off, cand_off;  // within a wave's region
+};
+
+__host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP) {
+  SelectLds s;
+  s.row_stride = P * D + 8;
+  s.chunk_bytes = kChunk * s.row_stride * 2;
+  const int trow = ((NB * 4) + 15) / 16 * 16;
+  s.trow_off = 0;
+  s.hist_off = trow;
+  s.cand_off = trow + 256 * 4;
+  s.wave_bytes = s.cand_off + KP * 8;
+  return s;
+}
+
+// Exclusive prefix sum across the wavefront.
+__device__ __forceinline__ uint32_t wave_excl_scan(uint32_t x, int lane) {
+  uint32_t incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), off, 64));
+    if (lane >= off) incl += y;
+  }
+  return incl - x;
+}
+
+template <int D, int P, int KP>
+__global__ __launch_bounds__(512) void select_kernel(
+    const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+    const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
+    int W, int n_hc, float scaling, int k_base, int k_slots, int want_sigma,
+    int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score) {
+  constexpr int KS = D / 32;
+  constexpr int R = KP / 64;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const SelectLds L = select_lds(P, D, NB, KP);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int nthreads = blockDim.x;
+
+  const int unit = blockIdx.x / n_hc;
+  const int hc = blockIdx.x % n_hc;
+  const int per_t = B * Hk;
+  const int t = Qt - 1 - unit / per_t;
+  const int b = (unit % per_t) / Hk;
+  const int g = (unit % per_t) % Hk;
+  const int jh = hc * W + wave;
+  const bool active = jh < grp;
+  const int h = g * grp + (active ? jh : 0);
+  const int H = Hk * grp;
+
+  uint16_t* chunk = reinterpret_cast<uint16_t*>(smem);
+  unsigned char* wreg = smem + L.chunk_bytes + wave * L.wave_bytes;
+  float* trow = reinterpret_cast<float*>(wreg + L.trow_off);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(wreg + L.hist_off);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(wreg + L.cand_off);
+
+  const int last_row = min(t * kBlock + kBlock - 1, N - 1);
+  const int n_vis = last_row / kBlock + 1;           // blocks 0 .. self(t)
+
+  // Q tile rows as MFMA A operands (zero rows past M, as F.pad in the reference)
+  bf16x8 qf[4][KS];
+  {
+    const uint16_t* qb = q + b * sq_b + h * sq_h;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int row = t * kBlock + 16 * mt + r16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[mt][ks] = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
+                                         : zero_bf16x8();
+    }
+  }
+
+  const uint16_t* pl = planes + (static_cast<int64_t>(b) * Hk + g) * NB * P * D;
+  const int pieces_per_blk = P * D / 8;
+  const int n_chunks = (n_vis + kChunk - 1) / kChunk;
+  for (int c = 0; c < n_chunks; ++c) {
+    __syncthreads();
+    for (int pi = threadIdx.x; pi < kChunk * pieces_per_blk; pi += nthreads) {
+      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
+      const int blk = c * kChunk + bl;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (blk < NB) v = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
+      *reinterpret_cast<u32x4*>(chunk + bl * L.row_stride + off * 8) = v;
+    }
+    __syncthreads();
+    if (active) {
+      f32x4 acc[4][2];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          bf16x8 bfr[2];
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            bfr[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
+                                                       p * D + 32 * ks + 8 * g4);
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            bf16x8 a = qf[mt][ks];
+            if (P == 2) {
+              // keep the sign split inside the loop (hoisting both halves of
+              // every Q fragment out of the chunk loop doubles their registers)
+              u32x4 raw = __builtin_bit_cast(u32x4, a);
+              asm volatile("" : "+v"(raw));
+              a = __builtin_bit_cast(bf16x8, raw);
+              a = (p == 0) ? bf16_pos(a) : bf16_neg(a);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma16x16x32(a, bfr[nt], acc[mt][nt]);
+          }
+        }
+      }
+      // tile max over the 64 rows: 16 in-lane values, then across the 4 lane groups
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i] * scaling);
+        mx = fmaxf(mx, shfl_xor_f(mx, 16));
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        const int blk = c * kChunk + 16 * nt + r16;
+        if (g4 == nt && blk < NB) trow[blk] = mx;
+      }
+    }
+  }
+  if (!active) return;   // no workgroup barrier follows
+  wave_lds_sync();
+  if (lane == 0) {
+    trow[0] = kFMax;
+    trow[n_vis - 1] = kFMax;
+  }
+  wave_lds_sync();
+
+  const int64_t row_id = (static_cast<int64_t>(b) * H + h) * Qt + t;
+  if (tile_score != nullptr) {
+    float* ts = tile_score + row_id * NB;
+    for (int i = lane; i < NB; i += 64) ts[i] = i < n_vis ? trow[i] : -INFINITY;
+  }
+
+  // ---- top-k_slots over the n_vis visible scores ------------------------
+  const int K = k_slots;
+  const int n_sel = min(n_vis, K);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  if (n_vis > K) {
+    uint32_t prefix = 0, pmask = 0;
+    int remaining = K;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = lane; i < 256; i += 64) hist[i] = 0;
+      wave_lds_sync();
+      for (int i = lane; i < n_vis; i += 64) {
+        const uint32_t key = float_key(trow[i]);
+        if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      wave_lds_sync();
+      // lane L holds bins 255-4L .. 252-4L (descending digit order)
+      uint32_t cnt[4], s = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { cnt[j] = hist[255 - 4 * lane - j]; s += cnt[j]; }
+      uint32_t cg = wave_excl_scan(s, lane);   // keys in strictly greater digits
+      int found = -1;
+      uint32_t rem_new = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (found < 0 && cg < static_cast<uint32_t>(remaining) &&
+            static_cast<uint32_t>(remaining) <= cg + cnt[j]) {
+          found = 255 - 4 * lane - j;
+          rem_new = remaining - cg;
+        }
+        cg += cnt[j];
+      }
+      const uint64_t who = __ballot(found >= 0);
+      const int src = __ffsll(static_cast<long long>(who)) - 1;
+      const int digit = __shfl(found, src, 64);
+      remaining = __shfl(static_cast<int>(rem_new), src, 64);
+      prefix |= static_cast<uint32_t>(digit) << shift;
+      pmask |= 0xFFu << shift;
+      wave_lds_sync();
+    }
+    const uint32_t tau = prefix;
+    const int need_eq = remaining;
+    const int n_gt = K - need_eq;
+    int cnt_gt = 0, cnt_eq = 0;
+    for (int base = 0; base < n_vis; base += 64) {
+      const int i = base + lane;
+      const uint32_t key = i < n_vis ? float_key(trow[i]) : 0u;
+      const bool gt = i < n_vis && key > tau;
+      const bool eq = i < n_vis && key == tau;
+      const uint64_t bg = __ballot(gt), be = __ballot(eq);
+      const uint64_t comp = (static_cast<uint64_t>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+      if (gt) {
+        const int pos = cnt_gt + __popcll(bg & lt_mask);
+        if (pos < n_gt) cand[pos] = comp;
+      }
+      if (eq) {
+        const int pos = cnt_eq + __popcll(be & lt_mask);
+        if (pos < need_eq) cand[n_gt + pos] = comp;
+      }
+      cnt_gt += __popcll(bg);
+      cnt_eq += __popcll(be);
+    }
+  } else {
+    for (int i = lane; i < n_vis; i += 64)
+      cand[i] = (static_cast<uint64_t>(float_key(trow[i])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+  }
+  wave_lds_sync();
+
+  uint64_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int e = lane + 64 * r;
+    v[r] = e < n_sel ? cand[e] : 0ull;
+  }
+  // bitonic sort, descending
+#pragma unroll
+  for (int kk = 2; kk <= KP; kk <<= 1) {
+#pragma unroll
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      uint64_t nv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int e = lane + 64 * r;
+        const uint64_t other = (j >= 64) ? v[r ^ (j >> 6)] : shfl_xor_u64(v[r], j);
+        const bool lower = (e & j) == 0;
+        const bool desc = (e & kk) == 0;
+        const bool keep_max = lower == desc;
+        const uint64_t mx = v[r] > other ? v[r] : other;
+        const uint64_t mn = v[r] > other ? other : v[r];
+        nv[r] = keep_max ? mx : mn;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r] = nv[r];
+    }
+  }
+
+  int32_t* out = kv_idx + row_id * K;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int e = lane + 64 * r;
+    if (e < K)
+      out[e] = e < n_sel ? static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(v[r])) : e;
+  }
+
+  if (want_sigma) {
+    auto val_at = [&](int e) -> float {
+      uint64_t x = 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (r == (e >> 6)) x = v[r];
+      const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(x >> 32), e & 63, 64));
+      return e < n_sel ? key_float(hi) : -INFINITY;
+    };
+    const float s_top = val_at(0);
+    const float a = val_at(k_base - 1);
+    const float cth = val_at(k_base);
+    float spread = s_top - cth;
+    if (spread < 1e-6f) spread = 1e-6f;     // clamp(min=1e-6); NaN stays NaN
+    const float sg = (a - cth) / spread;
+    if (lane == 0) sigma[row_id] = sg;
+  }
+}
+
+template <int D, int P, int KP>
+static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                                  const uint16_t* planes, int B, int H, int Hk, int M, int N,
+                                  float scaling, int k_base, int k_slots, int want_sigma,
+                                  int32_t* kv_idx, float* sigma, float* tile_score,
+                                  hipStream_t stream) {
+  const int NB = (N + kBlock - 1) / kBlock;
+  const int Qt = (M + kBlock - 1) / kBlock;
+  const int grp = H / Hk;
+  const SelectLds L = select_lds(P, D, NB, KP);
+  constexpr int kLdsMax = 160 * 1024;
+  int W = grp < 8 ? grp : 8;
+  while (W > 1 && L.chunk_bytes + W * L.wave_bytes > kLdsMax) --W;
+  if (L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
+  const int n_hc = (grp + W - 1) / W;
+  const size_t lds = L.chunk_bytes + static_cast<size_t>(W) * L.wave_bytes;
+  const int64_t wgs = static_cast<int64_t>(B) * Hk * Qt * n_hc;
+  auto kern = select_kernel<D, P, KP>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds));
+  if (e != hipSuccess) return e;
+  kern<<<dim3(static_cast<unsigned>(wgs)), 64 * W, lds, stream>>>(
+      q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, n_hc, scaling, k_base,
+      k_slots, want_sigma, kv_idx, sigma, tile_score);
+  return hipGetLastError();
+}
+
+template <int D, int P>
+static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                                   const uint16_t* planes, int B, int H, int Hk, int M, int N,
+                                   float scaling, int k_base, int k_slots, int want_sigma,
+                                   int32_t* kv_idx, float* sigma, float* tile_score,
+                                   hipStream_t stream) {
+#define UGBSA_SEL(KP_)                                                                    \
+  return launch_select_t<D, P, KP_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,  \
+                                    k_base, k_slots, want_sigma, kv_idx, sigma, tile_score, \
+                                    stream)
+  if (k_slots <= 64) UGBSA_SEL(64);
+  if (k_slots <= 128) UGBSA_SEL(128);
+  if (k_slots <= 256) UGBSA_SEL(256);
+  if (k_slots <= 512) UGBSA_SEL(512);
+#undef UGBSA_SEL
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_select(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                         const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
+                         int mode, float scaling, int k_base, int k_slots, int want_sigma,
+                         int32_t* kv_idx, float* sigma, float* tile_score,
+                         hipStream_t stream) {
+#define UGBSA_SELD(D_, P_)                                                                 \
+  return launch_select_kp<D_, P_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,    \
+                                  k_base, k_slots, want_sigma, kv_idx, sigma, tile_score,  \
+                                  stream)
+  const bool quest = mode == kModeQuest;
+  if (D == 64) { if (quest) UGBSA_SELD(64, 2); else UGBSA_SELD(64, 3); }
+  if (D == 128) { if (quest) UGBSA_SELD(128, 2); else UGBSA_SELD(128, 3); }
+  if (D == 256) { if (quest) UGBSA_SELD(256, 2); else UGBSA_SELD(256, 3); }
+#undef UGBSA_SELD
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ugbsa

@@ -1,0 +1,286 @@
+"""Block-sparse prefill attention selector + HF dispatch on MI355X.
+
+Drop-in for the v2 path of the reference's ``src/sparse_attention.py``: the
+same module-level ``SEL`` / ``PROF`` objects and field names, the same
+``_block_select_kv_idx_v2(query, key_states, scaling, block_m=64)`` and
+``block_sparse_attention(module, query, key, value, attention_mask, scaling,
+dropout=0.0, **kwargs)`` signatures, and the same
+``AttentionInterface.register("block_sparse", ...)`` at import.  Selection and
+attention run in hand-written gfx950 HIP kernels through ``_capi``:
+
+  kernel 1  ugbsa_block_summary  K-block mean / (min, max)        (:618-646)
+  kernel 2  ugbsa_select         scores, tile max, mask, forcing,
+                                 top-k, sigma                      (:638-707)
+  router    ugbsa_router         row mean, quantile / abs, sentinels (:708-725)
+  kernel 3  ugbsa_attn_fwd       block-sparse attention            (triton_block_attn.py)
+
+Everything is asynchronous on the current stream; like the reference, the v2
+path syncs the host only when ``SEL.log`` asks for diagnostics.
+
+Differences from the reference, by design:
+
+* Scores are fp32 (bf16 inputs, fp32 MFMA accumulation) rather than the model
+  dtype, and ``topk`` ties are broken by block index (the reference leaves the
+  order unspecified).  ``kv_idx`` therefore equals the reference selector run
+  on fp32 scores.
+* The dispatcher hands the selector and the kernel the un-repeated
+  ``[B, Hk, N, D]`` key/value tensors (GQA handled in-kernel) instead of
+  ``repeat_kv`` copies; ``_block_select_kv_idx_v2`` accepts either.
+* The v1 per-row path (``kernel_v2=False`` and the belief / rollout modes) is
+  not part of this build and raises ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+import _capi
+from block_attn import attn_workspace, block_sparse_attn_v2
+
+BLOCK = 64   # tokens per selection block (src/sparse_attention.py:51)
+
+
+class Selector:
+    """Global selector configuration + diagnostics (src/sparse_attention.py:54-138).
+
+    Same fields and defaults as the reference.  The v2 path reads ``mode``,
+    ``budget_blocks``, ``k_min``/``k_max``, ``router_mode``, ``router_grain``,
+    ``router_tau``, ``router_quantile``, ``router_score``, ``kernel_v2`` and
+    ``log``; the remaining knobs belong to the v1 / rollout research modes and
+    are kept so harness code that sets them keeps working.
+    """
+
+    def __init__(self):
+        self.mode = "dense"          # "dense"|"topk"|"belief"|"rollout"|"rollout_peek"|"router"|"quest"
+        self.budget_blocks = 32
+        self.top_p = 0.9
+        self.k_min, self.k_max = 8, 112
+        self.explore_bonus = 0.3
+        self.ema_alpha = 0.3
+        self.router_mode = "abs"     # "abs" | "quantile"
+        self.router_grain = "cell"   # "cell" | "row"
+        self.router_tau = 0.10
+        self.router_quantile = 0.20
+        self.router_score = "mean"   # "mean" | "quest"
+        self.kernel_v2 = False
+        self.peek_swap_w = 2
+        self.peek_rows_per_layer = 32
+        self.peek_layer_min = 0
+        self.peek_layer_max = 999
+        self.peek_metric = "peakedness"
+        self.peek_xh_threshold = 0.5
+        self.model_ref = None
+        self.hidden_at = {}
+        self.k_pool_at = {}
+        self.log = False
+        self.reset_log()
+
+    def reset_log(self):
+        self.kept_blocks = {}
+        self.budget_samples = []
+        self.selection_history = None
+        self.k_pool_at = {}
+        self.router_trigger_rate = []
+        self.router_eff_budget = []
+        self.router_margin_mean = []
+
+
+SEL = Selector()
+
+
+class _Profiler:
+    """Event profiler for block_sparse_attention internals (src/sparse_attention.py:141-183).
+
+    Opt-in (``PROF.enabled = True``); buckets ``dense_sdpa``, ``v2_select``,
+    ``v2_kernel``; ``summary()`` synchronises and returns calls / total / mean /
+    p50 ms per bucket.  Events are HIP events on the current stream.
+    """
+
+    def __init__(self):
+        self.enabled = False
+        self.events = {}
+
+    def reset(self):
+        self.events = {}
+
+    def start(self, name):
+        if not self.enabled or not torch.cuda.is_available():
+            return None
+        ev_s = torch.cuda.Event(enable_timing=True)
+        ev_e = torch.cuda.Event(enable_timing=True)
+        ev_s.record()
+        self.events.setdefault(name, []).append((ev_s, ev_e))
+        return ev_e
+
+    @staticmethod
+    def stop(ev_e):
+        if ev_e is not None:
+            ev_e.record()
+
+    def summary(self):
+        if not self.events:
+            return {}
+        torch.cuda.synchronize()
+        out = {}
+        for name, ev_list in self.events.items():
+            ms = sorted(s.elapsed_time(e) for s, e in ev_list)
+            out[name] = {"calls": len(ms), "total_ms": sum(ms),
+                         "mean_ms": sum(ms) / len(ms), "p50_ms": ms[len(ms) // 2]}
+        return out
+
+
+PROF = _Profiler()
+
+
+def budgets(n_blocks: int, sel: Selector = None):
+    """(k_base, k_slots) of the v2 selector — src/sparse_attention.py:688-695."""
+    sel = SEL if sel is None else sel
+    k_row = int(max(min(sel.k_max, sel.budget_blocks), sel.k_min))
+    k_base = min(2 * k_row, n_blocks)
+    k_slots = min(2 * k_base, n_blocks) if sel.mode == "router" else k_base
+    return k_base, k_slots
+
+
+@dataclass
+class SelectionResult:
+    kv_idx: torch.Tensor                 # int32 [B, H, Qt, k_slots]
+    k_base: int
+    k_slots: int
+    sigma: torch.Tensor | None = None     # fp32 [B, H, Qt] per-cell margin
+    sigma_eff: torch.Tensor | None = None  # after the row-grain mean
+    uncertain: torch.Tensor | None = None  # uint8 [B, H, Qt]
+    threshold: torch.Tensor | None = None  # fp32 [1]
+    tile_score: torch.Tensor | None = None  # fp32 [B, H, Qt, NB] (if asked)
+
+
+def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
+              want_tile_score=False) -> SelectionResult:
+    """Run kernels 1, 2 and the router; return kv_idx plus the router state."""
+    sel = SEL if sel is None else sel
+    assert block_m == BLOCK, "selection tiles are 64 rows"
+    assert query.is_cuda and query.dtype == torch.bfloat16, "bf16 HIP query required"
+    assert key_states.dtype == torch.bfloat16 and key_states.device == query.device
+    B, H, M, D = query.shape
+    Hk, N = key_states.shape[1], key_states.shape[2]
+    assert key_states.shape[0] == B and key_states.shape[3] == D and H % Hk == 0
+    dev = query.device
+    lib = _capi.lib()
+    stream = _capi.stream_ptr(dev)
+    query = _contig_rows(query)
+    key_states = _contig_rows(key_states)
+    n_blocks = (N + BLOCK - 1) // BLOCK
+    q_tiles = (M + block_m - 1) // block_m
+    k_base, k_slots = budgets(n_blocks, sel)
+    quest = sel.mode == "quest" or (sel.mode == "router" and sel.router_score == "quest")
+    mode = _capi.MODE_QUEST if quest else _capi.MODE_MEAN
+
+    planes = torch.empty(lib.ugbsa_summary_elems(B, Hk, N, D, mode), dtype=torch.bfloat16, device=dev)
+    _capi.check(lib.ugbsa_block_summary(key_states.data_ptr(), *key_states.stride(), B, Hk, N, D,
+                                        _capi.DTYPE_BF16, mode, planes.data_ptr(), stream),
+                "block summary")
+    is_router = sel.mode == "router" and k_base < k_slots
+    kv_idx = torch.empty(B, H, q_tiles, k_slots, dtype=torch.int32, device=dev)
+    sigma = torch.empty(B, H, q_tiles, dtype=torch.float32, device=dev) if is_router else None
+    tile_score = (torch.empty(B, H, q_tiles, n_blocks, dtype=torch.float32, device=dev)
+                  if want_tile_score else None)
+    _capi.check(lib.ugbsa_select(query.data_ptr(), *query.stride(), planes.data_ptr(),
+                                 B, H, Hk, M, N, D, _capi.DTYPE_BF16, mode, float(scaling),
+                                 k_base, k_slots, block_m, kv_idx.data_ptr(),
+                                 _capi.ptr(sigma), _capi.ptr(tile_score), stream),
+                "select")
+    res = SelectionResult(kv_idx, k_base, k_slots, sigma=sigma, tile_score=tile_score)
+    if is_router:
+        grain = _capi.GRAIN_ROW if sel.router_grain == "row" else _capi.GRAIN_CELL
+        rmode = _capi.ROUTER_QUANTILE if sel.router_mode == "quantile" else _capi.ROUTER_ABS
+        k_quant = max(1, int(float(sel.router_quantile) * sigma.numel()))
+        res.sigma_eff = torch.empty_like(sigma)
+        res.uncertain = torch.empty(sigma.shape, dtype=torch.uint8, device=dev)
+        res.threshold = torch.empty(1, dtype=torch.float32, device=dev)
+        _capi.check(lib.ugbsa_router(sigma.data_ptr(), B, H, q_tiles, grain, rmode,
+                                     float(sel.router_tau), k_quant, kv_idx.data_ptr(),
+                                     k_base, k_slots, n_blocks, res.sigma_eff.data_ptr(),
+                                     res.uncertain.data_ptr(), res.threshold.data_ptr(), stream),
+                    "router")
+    return res
+
+
+def _contig_rows(t):
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
+        t = t.contiguous()
+    return t
+
+
+def _block_select_kv_idx_v2(query, key_states, scaling, block_m=64):
+    """v2 selection: kv_idx [B, H, Q_tiles, k_slots] int32, built on the GPU.
+
+    Same contract as src/sparse_attention.py:588-748.  ``key_states`` may be
+    the repeat_kv'd [B, H, N, D] tensor (as the reference passes) or the GQA
+    [B, Hk, N, D] one.
+    """
+    res = select_v2(query, key_states, scaling, block_m)
+    kv_idx = res.kv_idx
+    if SEL.log:
+        if res.uncertain is not None:
+            SEL.router_trigger_rate.append(float(res.uncertain.float().mean().item()))
+        n_blocks = (key_states.shape[-2] + BLOCK - 1) // BLOCK
+        last = kv_idx[0, :, -1, :].long().flatten()
+        last = last[last < n_blocks]
+        kept = torch.zeros(n_blocks, dtype=torch.bool, device=kv_idx.device)
+        kept.scatter_(0, last, True)
+        layer_idx = len(SEL.kept_blocks)
+        SEL.kept_blocks[layer_idx] = kept.cpu()
+        SEL.budget_samples.append(float(res.k_slots))
+    return kv_idx
+
+
+def block_sparse_attention(module, query, key, value, attention_mask,
+                           scaling, dropout=0.0, **kwargs):
+    """HF attention function (src/sparse_attention.py:751-788).
+
+    query [B, H, S, D]; key / value [B, Hk, S, D] as transformers passes them
+    (before repeat_kv).  Dense SDPA for ``mode == "dense"`` or decode (Q == 1);
+    the HIP v2 path for topk / router / quest with ``SEL.kernel_v2``.  Returns
+    ``(attn_output [B, S, H, D] contiguous, None)``.
+    """
+    Q = query.shape[-2]
+    is_prefill = Q > 1
+    H, Hk = query.shape[1], key.shape[1]
+
+    if SEL.mode == "dense" or Q == 1:
+        ev = PROF.start("dense_sdpa") if is_prefill else None
+        out = F.scaled_dot_product_attention(query, key, value, is_causal=Q > 1,
+                                             scale=scaling, enable_gqa=H != Hk)
+        PROF.stop(ev)
+        return out.transpose(1, 2).contiguous(), None
+
+    if SEL.kernel_v2 and SEL.mode in ("topk", "router", "quest"):
+        ev = PROF.start("v2_select") if is_prefill else None
+        kv_idx = _block_select_kv_idx_v2(query, key, scaling)   # resolved at call time
+        PROF.stop(ev)
+        ev = PROF.start("v2_kernel") if is_prefill else None
+        B, _, S, D = query.shape
+        out = torch.empty(B, S, H, D, dtype=query.dtype, device=query.device)
+        ws = attn_workspace(B, Hk, key.shape[-2], D, query.device)
+        block_sparse_attn_v2(query, key, value, kv_idx, scale=scaling, block_n=BLOCK,
+                             out=out.transpose(1, 2), workspace=ws)
+        PROF.stop(ev)
+        return out, None
+
+    raise NotImplementedError(
+        f"SEL.mode={SEL.mode!r} with kernel_v2={SEL.kernel_v2}: the v1 per-row "
+        "path is not built on MI355X; use kernel_v2=True with topk/router/quest")
+
+
+def _register():
+    try:
+        from transformers import AttentionInterface
+    except ImportError:   # the kernels stay usable without transformers
+        return False
+    AttentionInterface.register("block_sparse", block_sparse_attention)
+    return True
+
+
+REGISTERED = _register()
