@@ -1,0 +1,373 @@
+#!/usr/bin/env python
+"""Sparse-prefill benchmark on one MI355X (BASELINE.json metric).
+
+A step is one sparse prefill attention layer over inputs already resident in
+HBM: K-block summaries -> fused select (scores, tile max, top-k, sigma) ->
+router (quantile, sentinels) -> K/V operand layout -> block-sparse attention.
+``value`` is ms/layer at BASELINE configs[1] (Qwen2.5-7B-1M layer, 32K,
+router-on-Quest 64 -> 128); the 128K layer and the dense
+comparators are reported in the same line.  Inputs are synthetic (seeded
+N(0,1) with planted needle blocks, synth.py), drawn on the GPU.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "uncertainty-gated-block-sparse-attention_amd")
+sys.path.insert(0, PKG)
+
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", default="c2")
+    p.add_argument("--c3-layers", type=int, default=28,
+                   help="stacked independent 128K layers for the configs[2] sweep (0 = skip)")
+    p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=20.0,
+                   help="target CPU work of the bounded baseline sample")
+    return p.parse_args()
+
+
+class LayerRunner:
+    """Preallocated buffers + the five launches of one sparse prefill layer."""
+
+    def __init__(self, cfg, q, k, v, sel_fields=None):
+        import torch
+        import _capi
+        import sparse_attention as sa
+        self.torch, self.capi, self.lib = torch, _capi, _capi.lib()
+        self.cfg = cfg
+        self.q, self.k, self.v = q, k, v
+        B, H, S, D = q.shape
+        Hk = k.shape[1]
+        self.B, self.H, self.Hk, self.S, self.D = B, H, Hk, S, D
+        sel = sa.Selector()
+        for f, val in (sel_fields or cfg.sel_fields()).items():
+            setattr(sel, f, val)
+        self.sel = sel
+        self.NB = self.Qt = (S + 63) // 64
+        self.k_base, self.k_slots = sa.budgets(self.NB, sel)
+        quest = sel.mode == "quest" or (sel.mode == "router" and sel.router_score == "quest")
+        self.mode = _capi.MODE_QUEST if quest else _capi.MODE_MEAN
+        self.router = sel.mode == "router" and self.k_base < self.k_slots
+        dev = q.device
+        self.planes = torch.empty(self.lib.ugbsa_summary_elems(B, Hk, S, D, self.mode),
+                                  dtype=torch.bfloat16, device=dev)
+        self.kv_idx = torch.empty(B, H, self.Qt, self.k_slots, dtype=torch.int32, device=dev)
+        self.sigma = torch.empty(B, H, self.Qt, dtype=torch.float32, device=dev)
+        self.sigma_eff = torch.empty_like(self.sigma)
+        self.unc = torch.empty(B, H, self.Qt, dtype=torch.uint8, device=dev)
+        self.thr = torch.empty(1, dtype=torch.float32, device=dev)
+        self.ws = torch.empty(self.lib.ugbsa_attn_workspace_elems(B, Hk, S, D),
+                              dtype=torch.bfloat16, device=dev)
+        self.out = torch.empty_like(q)
+        self.k_quant = max(1, int(float(sel.router_quantile) * B * H * self.Qt))
+        self.grain = _capi.GRAIN_ROW if sel.router_grain == "row" else _capi.GRAIN_CELL
+        self.rmode = _capi.ROUTER_QUANTILE if sel.router_mode == "quantile" else _capi.ROUTER_ABS
+        self.names = ["summary", "select", "router", "prepare_kv", "attention"]
+
+    def step(self, ev=None):
+        """One layer; ev: list of 6 events recorded between the launches."""
+        c, L, s = self.capi, self.lib, self.capi.stream_ptr(self.q.device)
+        q, k, v = self.q, self.k, self.v
+        B, H, Hk, S, D = self.B, self.H, self.Hk, self.S, self.D
+        rec = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
+        rec(0)
+        c.check(L.ugbsa_block_summary(k.data_ptr(), *k.stride(), B, Hk, S, D, c.DTYPE_BF16,
+                                      self.mode, self.planes.data_ptr(), s), "summary")
+        rec(1)
+        c.check(L.ugbsa_select(q.data_ptr(), *q.stride(), self.planes.data_ptr(), B, H, Hk, S, S, D,
+                               c.DTYPE_BF16, self.mode, float(self.cfg.scaling), self.k_base,
+                               self.k_slots, 64, self.kv_idx.data_ptr(),
+                               self.sigma.data_ptr() if self.router else None, None, s), "select")
+        rec(2)
+        if self.router:
+            c.check(L.ugbsa_router(self.sigma.data_ptr(), B, H, self.Qt, self.grain, self.rmode,
+                                   float(self.sel.router_tau), self.k_quant, self.kv_idx.data_ptr(),
+                                   self.k_base, self.k_slots, self.NB, self.sigma_eff.data_ptr(),
+                                   self.unc.data_ptr(), self.thr.data_ptr(), s), "router")
+        rec(3)
+        c.check(L.ugbsa_attn_prepare_kv(k.data_ptr(), *k.stride(), v.data_ptr(), *v.stride(),
+                                        B, Hk, S, D, c.DTYPE_BF16, 64, self.ws.data_ptr(), s),
+                "prepare_kv")
+        rec(4)
+        self.attention(self.kv_idx)
+        rec(5)
+
+    def attention(self, kv_idx):
+        c, L, s = self.capi, self.lib, self.capi.stream_ptr(self.q.device)
+        q, k, o = self.q, self.k, self.out
+        c.check(L.ugbsa_attn_fwd(q.data_ptr(), *q.stride(), k.data_ptr(), *k.stride(),
+                                 None, 0, 0, 0, 1, kv_idx.data_ptr(), *kv_idx.stride(),
+                                 self.B, self.H, self.Hk, self.S, self.S, self.D, c.DTYPE_BF16,
+                                 kv_idx.shape[2], kv_idx.shape[3], 64, float(self.cfg.scaling),
+                                 o.data_ptr(), *o.stride(), self.ws.data_ptr(), s), "attention")
+
+    def attended_flops(self, kv_idx=None) -> float:
+        """Executed attention FLOPs: 4 * 64 * 64 * D per visited (tile, block)."""
+        torch = self.torch
+        kv = self.kv_idx if kv_idx is None else kv_idx
+        t = torch.arange(kv.shape[2], device=kv.device).view(1, 1, -1, 1)
+        ok = (kv >= 0) & (kv < self.NB) & (kv <= t)
+        return float(ok.sum().item()) * 4.0 * 64 * 64 * self.D
+
+    def select_bytes(self) -> dict:
+        """Algorithmic HBM bytes of kernels 1 and 2 (one launch each)."""
+        B, H, Hk, S, D, NB = self.B, self.H, self.Hk, self.S, self.D, self.NB
+        P = 2 if self.mode == self.capi.MODE_QUEST else 3
+        planes = B * Hk * NB * P * D * 2
+        k1 = B * Hk * S * D * 2 + planes
+        k2 = B * H * S * D * 2 + planes + B * H * self.Qt * self.k_slots * 4 + B * H * self.Qt * 4
+        return {"summary": k1, "select": k2}
+
+    def select_flops(self) -> float:
+        """Scoring FLOPs over causally visible blocks, one summary contraction
+        per backbone (Quest 2, mean 1), as BASELINE counts them."""
+        n_sum = 2 if self.mode == self.capi.MODE_QUEST else 1
+        vis = self.Qt * (self.Qt + 1) // 2
+        return 2.0 * self.D * 64 * self.B * self.H * n_sum * vis
+
+
+def timed(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, (time.perf_counter() - t0) * 1e3 / steps
+
+
+def run_layer_bench(runner, steps, warmup, torch):
+    """Timed region of `steps` layers; returns ms/step and per-kernel mean ms."""
+    for _ in range(warmup):
+        runner.step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        runner.step(evs[i])
+    end.record()
+    torch.cuda.synchronize()
+    total = start.elapsed_time(end) / steps
+    per = {}
+    for j, name in enumerate(runner.names):
+        per[name] = sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps
+    return total, per
+
+
+def dense_sdpa_ms(q, k, v, scaling, torch, steps=3):
+    """torch SDPA causal bf16 on the repeat_kv'd heads (the reference's dense path)."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    rep = q.shape[1] // k.shape[1]
+    kr = k.repeat_interleave(rep, dim=1)
+    vr = v.repeat_interleave(rep, dim=1)
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel([backend]):
+                fn = lambda: F.scaled_dot_product_attention(q, kr, vr, is_causal=True, scale=scaling)
+                ms, _ = timed(fn, steps, 1, torch)
+            return ms, backend.name
+        except RuntimeError:
+            continue
+    return None, None
+
+
+def dense_kernel3_ms(runner, torch, steps=3):
+    """The build's kernel 3 on a full causal kv_idx (case A) — the MFMA dense comparator."""
+    B, H, Qt = runner.B, runner.H, runner.Qt
+    full = torch.arange(Qt, dtype=torch.int32, device=runner.q.device).view(1, 1, 1, Qt)
+    full = full.expand(B, H, Qt, Qt).contiguous()
+    ms, _ = timed(lambda: runner.attention(full), steps, 1, torch)
+    flops = 4.0 * B * H * runner.D * 64 * 64 * Qt * (Qt + 1) / 2
+    del full
+    return ms, flops
+
+
+def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
+    """The CPU oracle (numpy fp32) timed on a bounded sample of the same layer:
+    the full selector for one KV group (its query heads) and masked dense
+    attention (reference_attn cost) for sampled tiles of one head; both scaled
+    to one full layer."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    sys.path.insert(0, ROOT)
+    from oracle import attention as OA
+    from oracle import selector as OS
+    import sparse_attention as sa
+
+    grp = cfg.Hq // cfg.Hkv
+    qs = q[:, :grp].float().cpu().numpy()
+    ks = k[:, :1].float().cpu().numpy()
+    sel = sa.Selector()
+    for f, val in cfg.sel_fields().items():
+        setattr(sel, f, val)
+    ocfg = OS.SelectorConfig.from_selector(sel)
+    t0 = time.perf_counter()
+    OS.select_kv_idx_v2(qs, ks, cfg.scaling, ocfg)
+    sel_s = (time.perf_counter() - t0) * cfg.Hkv
+    # masked dense attention for one head: tiles sampled evenly, cost-weighted
+    qt = kv_idx.shape[2]
+    q0 = q[:, :1].float().cpu().numpy()
+    k0 = k[:, :1].float().cpu().numpy()
+    v0 = v[:, :1].float().cpu().numpy()
+    kv0 = kv_idx[:, :1].cpu().numpy()
+    total_cost = qt * (qt + 1) / 2                      # sum over tiles of (t + 1) key blocks
+    tiles = list(range(qt - 1, -1, -7))                  # spread over the causal range
+    t0 = time.perf_counter()
+    done = []
+    for t in tiles:                                      # until the time budget is spent
+        OA.masked_tile_attention(q0, k0, v0, kv0, cfg.scaling, tiles=[t])
+        done.append(t)
+        if time.perf_counter() - t0 > budget_s:
+            break
+    att_sample_s = time.perf_counter() - t0
+    att_s = att_sample_s * total_cost / sum(t + 1 for t in done) * cfg.Hq
+    threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    return {
+        "value": round((sel_s + att_s) * 1e3, 1),
+        "unit": "ms/layer",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"numpy fp32 oracle on {cfg.name}: full v2 selector for 1 of {cfg.Hkv} KV groups "
+                   f"({sel_s / cfg.Hkv:.1f} s, x{cfg.Hkv}); masked dense attention (reference_attn "
+                   f"cost) for {len(done)} of {qt} tiles of 1 of {cfg.Hq} heads "
+                   f"({att_sample_s:.1f} s, scaled by causal cost and x{cfg.Hq})"),
+        "select_ms": round(sel_s * 1e3, 1),
+        "attention_ms": round(att_s * 1e3, 1),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the hot path shards by KV-head group; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = synth.CONFIGS[args.config]
+    t_gen = time.perf_counter()
+    q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
+    gen_s = time.perf_counter() - t_gen
+    runner = LayerRunner(cfg, q, k, v)
+    ms_step, per = run_layer_bench(runner, args.steps, args.warmup, torch)
+    attn_flops = runner.attended_flops()
+    sel_bytes = runner.select_bytes()
+    attn_tflops = attn_flops / (per["attention"] * 1e-3) / 1e12
+    select_ms = per["summary"] + per["select"] + per["router"]
+    res = {
+        "metric": "sparse prefill ms/layer at 32K/128K vs dense; attended TFLOP/s; % MFMA peak",
+        "value": round(ms_step, 4),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V with planted needle blocks, synth.make_layer_fast on the GPU)",
+        "config": {"workload": f"{cfg.name}: BASELINE configs[{cfg.index}] — one causal prefill "
+                               f"attention layer, B={cfg.B} Hq={cfg.Hq} Hkv={cfg.Hkv} S={cfg.S} "
+                               f"D={cfg.D}, {cfg.mode}-on-{cfg.router_score} "
+                               f"k_base={runner.k_base} k_slots={runner.k_slots} "
+                               f"q={cfg.router_quantile} {cfg.router_grain}-grain",
+                   "seq_len": cfg.S, "global_batch": cfg.B},
+        "kernels_ms": {k_: round(v_, 4) for k_, v_ in per.items()},
+        "select_ms": round(select_ms, 4),
+        "attended_tflop": round(attn_flops / 1e12, 4),
+        "attended_tflops": round(attn_tflops, 1),
+        "trigger_rate": round(float(runner.unc.float().mean().item()), 4) if runner.router else None,
+        "hbm_gbs": {
+            "summary": round(sel_bytes["summary"] / (per["summary"] * 1e-3) / 1e9, 1),
+            "select": round(sel_bytes["select"] / (per["select"] * 1e-3) / 1e9, 1),
+        },
+        "select_mfma_frac": round(runner.select_flops() / (per["select"] * 1e-3) / 1e12
+                                  / PEAK_BF16_TFLOPS, 4),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attn_fwd_kernel",
+            "achieved": round(attn_tflops, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "gen_s": round(gen_s, 1),
+    }
+    if not args.no_dense:
+        sd_ms, backend = dense_sdpa_ms(q, k, v, cfg.scaling, torch)
+        k3_ms, k3_flops = dense_kernel3_ms(runner, torch)
+        dense_best = min(x for x in (sd_ms, k3_ms) if x is not None)
+        res["dense"] = {"sdpa_ms": None if sd_ms is None else round(sd_ms, 3), "sdpa_backend": backend,
+                        "kernel3_full_ms": round(k3_ms, 3),
+                        "kernel3_full_tflops": round(k3_flops / (k3_ms * 1e-3) / 1e12, 1),
+                        "ratio_sparse_vs_dense": round(ms_step / dense_best, 4)}
+    kv_for_cpu = runner.kv_idx.clone()
+    del runner
+    if args.c3_layers > 0 and args.config != "c3":
+        c3 = synth.CONFIGS["c3"]
+        layers = []
+        for layer in range(args.c3_layers):
+            lq, lk, lv = synth.make_layer_fast(c3, layer, device=dev)
+            layers.append(LayerRunner(c3, lq, lk, lv))
+        torch.cuda.synchronize()
+        sweep_steps = max(1, min(args.steps, 3))
+
+        def sweep():
+            for r in layers:
+                r.step()
+        ms_sweep, _ = timed(sweep, sweep_steps, 1, torch)
+        r0 = layers[0]
+        ms1, per3 = run_layer_bench(r0, max(3, args.steps // 2), 1, torch)
+        fl3 = r0.attended_flops()
+        tf3 = fl3 / (per3["attention"] * 1e-3) / 1e12
+        c3res = {"layers": args.c3_layers, "ms_per_layer": round(ms_sweep / args.c3_layers, 3),
+                 "single_layer_ms": round(ms1, 3),
+                 "kernels_ms": {k_: round(v_, 3) for k_, v_ in per3.items()},
+                 "attended_tflop": round(fl3 / 1e12, 3), "attended_tflops": round(tf3, 1),
+                 "mfma_frac": round(tf3 / PEAK_BF16_TFLOPS, 4)}
+        if not args.no_dense:
+            sd3, _ = dense_sdpa_ms(r0.q, r0.k, r0.v, c3.scaling, torch, steps=2)
+            k33, k3f = dense_kernel3_ms(r0, torch, steps=2)
+            best = min(x for x in (sd3, k33) if x is not None)
+            c3res.update({"dense_sdpa_ms": None if sd3 is None else round(sd3, 2),
+                          "dense_kernel3_ms": round(k33, 2),
+                          "dense_kernel3_tflops": round(k3f / (k33 * 1e-3) / 1e12, 1),
+                          "ratio_sparse_vs_dense": round((ms_sweep / args.c3_layers) / best, 4)})
+        res["c3"] = c3res
+        del layers
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(cfg, q, k, v, kv_for_cpu, args.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -86,15 +86,28 @@ int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode,
                  int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots, int NB,
                  float* sigma_eff, uint8_t* uncertain, float* threshold, void* stream);
 
-/* Number of bf16 elements of the attention workspace (V transposed per block). */
+/* Number of bf16 elements of the attention workspace: the K and V operand
+ * copies of ugbsa_attn_prepare_kv (2 * B * Hk * NB * 64 * D). */
 int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D);
+
+/* K and V of every 64-key block re-laid in the attention kernel's operand
+ * order (for block_m 64 at head_dim 64/128: K and V^T as 1 KiB per-lane slabs
+ * per 32-key half block; otherwise V^T per block), keys past N zero.  Part of
+ * block_sparse_attn_v2's work (src/triton_block_attn.py:267-298), exposed so
+ * a caller can prepare K/V once and time or reuse it. */
+int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                          const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                          int B, int Hk, int N, int D, int dtype, int block_m, void* workspace,
+                          void* stream);
 
 /* Kernel 3 — block-sparse causal attention over kv_idx.
  * Replaces block_sparse_attn_v2 (src/triton_block_attn.py:267-298) and its
  * kernel _fwd_kernel_v2 (:184-264).  q [B, H, M, D], k/v [B, Hk, N, D] bf16
  * (Hk may equal H, as after repeat_kv), kv_idx [B, H, Qt, k_slots] int32 with
  * Qt = ceil(M / block_m), block_m 64 or 32, sentinel NB skipped; out
- * [B, H, M, D] bf16 with arbitrary strides (head_dim stride 1). */
+ * [B, H, M, D] bf16 with arbitrary strides (head_dim stride 1).  v may be
+ * NULL when workspace already holds ugbsa_attn_prepare_kv(k, v, block_m);
+ * otherwise the preparation runs first, on the same stream. */
 int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
                    const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                    const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,

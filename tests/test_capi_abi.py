@@ -40,7 +40,7 @@ def test_size_queries(lib):
     # [B, Hk, NB, P, D]: c3 Quest = 1 * 4 * 2048 * 2 * 128
     assert lib.ugbsa_summary_elems(1, 4, 131072, 128, _capi.MODE_QUEST) == 4 * 2048 * 2 * 128
     assert lib.ugbsa_summary_elems(1, 2, 1000, 64, _capi.MODE_MEAN) == 2 * 16 * 3 * 64
-    assert lib.ugbsa_attn_workspace_elems(1, 4, 1000, 128) == 4 * 16 * 64 * 128
+    assert lib.ugbsa_attn_workspace_elems(1, 4, 1000, 128) == 2 * 4 * 16 * 64 * 128
 
 
 def test_argument_errors_are_reported_without_launch(lib):

@@ -67,7 +67,7 @@ int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode) {
 
 int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D) {
   const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
-  return static_cast<int64_t>(B) * Hk * nb * ugbsa::kBlock * D;
+  return 2 * static_cast<int64_t>(B) * Hk * nb * ugbsa::kBlock * D;   // K and V operand copies
 }
 
 int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
@@ -129,6 +129,27 @@ int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode,
                     "router");
 }
 
+int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                          const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                          int B, int Hk, int N, int D, int dtype, int block_m, void* workspace,
+                          void* stream) {
+  int rc = check_dims(B, Hk, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("k", k, sk_b, sk_h, sk_n, sk_d))) return rc;
+  if ((rc = check_bf16_operand("v", v, sv_b, sv_h, sv_n, sv_d))) return rc;
+  if (N < 1) return fail(UGBSA_EARG, "N must be positive");
+  if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
+  if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace must be a 16-byte aligned buffer");
+  if (ugbsa_attn_workspace_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
+    return fail(UGBSA_EARG, "one KV head's K/V copy exceeds 4 GiB (N=%d, D=%d)", N, D);
+  return hip_result(ugbsa::launch_attn_prepare(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n,
+                                               static_cast<const uint16_t*>(v), sv_b, sv_h, sv_n,
+                                               B, Hk, N, D, block_m,
+                                               static_cast<uint16_t*>(workspace),
+                                               static_cast<hipStream_t>(stream)),
+                    "attn_prepare_kv");
+}
+
 int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
                    const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                    const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
@@ -140,7 +161,7 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
   if (rc) return rc;
   if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
   if ((rc = check_bf16_operand("k", k, sk_b, sk_h, sk_n, sk_d))) return rc;
-  if ((rc = check_bf16_operand("v", v, sv_b, sv_h, sv_n, sv_d))) return rc;
+  if (v != nullptr && (rc = check_bf16_operand("v", v, sv_b, sv_h, sv_n, sv_d))) return rc;
   if (out == nullptr) return fail(UGBSA_EARG, "out is null");
   if (so_d != 1 || (reinterpret_cast<uintptr_t>(out) & 7u) || so_b % 4 || so_h % 4 || so_m % 4)
     return fail(UGBSA_ELAYOUT, "out: head_dim stride 1, 8-byte aligned rows required");
@@ -152,8 +173,16 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
   if (k_slots < 1) return fail(UGBSA_EARG, "k_slots must be positive");
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* vt = static_cast<uint16_t*>(workspace);
-  hipError_t e = ugbsa::launch_v_block_transpose(static_cast<const uint16_t*>(v), sv_b, sv_h, sv_n, B, Hk, N, D, vt, st);
-  if (e != hipSuccess) return hip_result(e, "v_block_transpose");
+  if (static_cast<int64_t>(N) * sk_n * 2 > 0xFFFFFFFFLL || ugbsa_attn_workspace_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
+    return fail(UGBSA_EARG, "one KV head's K rows exceed the 4 GiB buffer-load range");
+  if (k_slots > 16384 && block_m == 64 && D <= 128)
+    return fail(UGBSA_EARG, "k_slots=%d exceeds the 16384-slot kv list of the attention kernel", k_slots);
+  if (v != nullptr) {   // NULL: the workspace already holds ugbsa_attn_prepare_kv's output
+    hipError_t e = ugbsa::launch_attn_prepare(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n,
+                                              static_cast<const uint16_t*>(v), sv_b, sv_h, sv_n,
+                                              B, Hk, N, D, block_m, vt, st);
+    if (e != hipSuccess) return hip_result(e, "attn_prepare_kv");
+  }
   return hip_result(ugbsa::launch_attn_fwd(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
                                            static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, vt,
                                            kv_idx, si_b, si_h, si_t, B, H, Hk, M, N, D, Qt,

@@ -62,12 +62,51 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 pairs -> bf16 with v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 __device__ __forceinline__ bf16x8 pack_bf16x8(const float* f) {
-  i16x8 v;
+  u32x4 w;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = static_cast<short>(f32_to_bf16(f[j]));
+  for (int j = 0; j < 4; ++j) w[j] = cvt_pk_bf16(f[2 * j], f[2 * j + 1]);
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// Raw buffer resource over [base, base + bytes): loads at byte offsets
+// outside the range return zeros (no fault, no branch).  Word 3 = 0x00020000
+// is the untyped raw-buffer configuration of gfx9-family parts.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+// 16 bytes at (voffset + soffset) of a raw buffer.
+__device__ __forceinline__ bf16x8 buffer_load_bf16x8(__amdgpu_buffer_rsrc_t r, uint32_t voffset,
+                                                    uint32_t soffset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voffset),
+                                                        static_cast<int>(soffset), 0);
   return __builtin_bit_cast(bf16x8, v);
 }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Asynchronous 16-byte-per-lane copy of a raw buffer into LDS: lane L's
+// 16 bytes land at lds + 16 * L.  Completion is tracked with vmcnt; the
+// compiler waits on the destination object before LDS reads of it.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds,
+                                                  uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(lds), 16,
+                                           static_cast<int>(voffset), static_cast<int>(soffset),
+                                           0, 0);
+}
+
+// s_waitcnt lgkmcnt(0): every LDS read of this wave has returned.
+__device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Monotone uint32 key of an fp32 value (larger float -> larger key); NaN is
 // mapped above +inf, matching torch.topk / kthvalue's NaN-is-largest order.

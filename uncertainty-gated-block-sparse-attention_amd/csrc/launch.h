@@ -36,9 +36,10 @@ hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, in
                          int NB, float* sigma_eff, uint8_t* uncertain, float* threshold,
                          hipStream_t stream);
 
-hipError_t launch_v_block_transpose(const uint16_t* v, int64_t sv_b, int64_t sv_h, int64_t sv_n,
-                                    int B, int Hk, int N, int D, uint16_t* vt,
-                                    hipStream_t stream);
+hipError_t launch_attn_prepare(const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                               const uint16_t* v, int64_t sv_b, int64_t sv_h, int64_t sv_n,
+                               int B, int Hk, int N, int D, int block_m, uint16_t* ws,
+                               hipStream_t stream);
 
 hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                            const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,

@@ -122,3 +122,52 @@ def make_layer(cfg: LayerConfig, layer: int = 0, *, S: int | None = None,
         q = rms_norm(q)
         k = rms_norm(k)
     return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def make_layer_fast(cfg: LayerConfig, layer: int = 0, *, device="cuda", dtype=None,
+                    S: int | None = None):
+    """Same structure as ``make_layer`` in a handful of device kernels (for
+    benchmarks at full scale): each tile t still plants min(n, t-1) distinct
+    needles in blocks 1 .. t-1 per KV head, the last tile to pick a block
+    wins, and a planted block gets 0.8 * (its winning tile's group-mean query)
+    + 0.6 * N(0, 1).  Draws differ from ``make_layer`` (a different order of
+    random calls), so parity fixtures use ``make_layer``."""
+    S = cfg.S if S is None else S
+    dtype = cfg.dtype if dtype is None else dtype
+    B, Hq, Hkv, D = cfg.B, cfg.Hq, cfg.Hkv, cfg.D
+    grp = Hq // Hkv
+    g = torch.Generator(device=device).manual_seed(1000 * cfg.index + layer)
+    q = torch.randn(B, Hq, S, D, generator=g, device=device)
+    k = torch.randn(B, Hkv, S, D, generator=g, device=device)
+    v = torch.randn(B, Hkv, S, D, generator=g, device=device)
+    qt = S // BLOCK
+    if cfg.needles > 0 and qt > 2:
+        full = qt * BLOCK
+        qm = q[:, :, :full].reshape(B, Hkv, grp, qt, BLOCK, D).mean(dim=(2, 4))  # [B,Hkv,Qt,D]
+        t = torch.arange(qt, device=device)
+        # rank random keys among blocks 1 .. t-1 of each (tile, head); pick the n smallest
+        r = torch.rand(qt, Hkv, qt, generator=g, device=device)
+        blk = torch.arange(qt, device=device)
+        ok = (blk[None, :] >= 1) & (blk[None, :] <= t[:, None] - 1)          # [Qt, NB]
+        r = torch.where(ok[:, None, :], r, torch.full_like(r, 2.0))
+        n = min(cfg.needles, qt)
+        picks = r.topk(n, dim=-1, largest=False).indices                     # [Qt, Hkv, n]
+        valid = torch.gather(ok[:, None, :].expand(qt, Hkv, qt), 2, picks)   # fewer than n early
+        tile = t[:, None, None].expand_as(picks)
+        head = torch.arange(Hkv, device=device)[None, :, None].expand_as(picks)
+        win = torch.full((Hkv, qt), -1, dtype=torch.long, device=device)
+        win.view(-1).scatter_reduce_(0, (head * qt + picks)[valid], tile[valid], reduce="amax")
+        noise = torch.randn(B, Hkv, qt, BLOCK, D, generator=g, device=device)
+        planted = win >= 0                                                    # [Hkv, NB]
+        src = qm[:, torch.arange(Hkv, device=device)[:, None], win.clamp(min=0)]  # [B,Hkv,NB,D]
+        val = 0.8 * src[:, :, :, None, :] + 0.6 * noise
+        kb = k[:, :, :full].view(B, Hkv, qt, BLOCK, D)
+        kb[:, planted] = val[:, planted]
+    if cfg.outlier_frac > 0:
+        n_out = round(cfg.outlier_frac * D)
+        ch = torch.randperm(D, generator=g, device=device)[:n_out]
+        k[..., ch] *= 4.0
+    if cfg.qk_norm:
+        q = rms_norm(q)
+        k = rms_norm(k)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
