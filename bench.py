@@ -40,6 +40,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
                    help="target CPU work of the bounded baseline sample")
+    p.add_argument("--pmc-run", action="store_true",
+                   help="untimed driver for rocprofv3 --pmc: --steps layers of the workload, "
+                        "then two copies of a 1 GiB tensor (counter calibration)")
     return p.parse_args()
 
 
@@ -143,7 +146,19 @@ class LayerRunner:
         return 2.0 * self.D * 64 * self.B * self.H * n_sum * vis
 
 
+def warm_clocks(fn, torch, seconds=1.0):
+    """Run fn until `seconds` of wall time have passed: MI355X clocks ramp
+    over a few hundred milliseconds of sustained work, so a handful of
+    warm-up steps alone under-reports steady-state speed."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn()
+        torch.cuda.synchronize()
+
+
 def timed(fn, steps, warmup, torch):
+    warm_clocks(fn, torch, 0.5)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -159,6 +174,7 @@ def timed(fn, steps, warmup, torch):
 
 def run_layer_bench(runner, steps, warmup, torch):
     """Timed region of `steps` layers; returns ms/step and per-kernel mean ms."""
+    warm_clocks(runner.step, torch)
     for _ in range(warmup):
         runner.step()
     torch.cuda.synchronize()
@@ -235,7 +251,8 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
     v0 = v[:, :1].float().cpu().numpy()
     kv0 = kv_idx[:, :1].cpu().numpy()
     total_cost = qt * (qt + 1) / 2                      # sum over tiles of (t + 1) key blocks
-    tiles = list(range(qt - 1, -1, -7))                  # spread over the causal range
+    # every 7th tile first, then the next interleave, ... : spread over the causal range
+    tiles = [t for off in range(7) for t in range(qt - 1 - off, -1, -7)]
     t0 = time.perf_counter()
     done = []
     for t in tiles:                                      # until the time budget is spent
@@ -260,6 +277,35 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
     }
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "attn_fwd_c2_traffic.md")
+
+
+def measured_traffic(cfg_name):
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (calibrated against a 1 GiB copy)."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith(f"traffic_bytes attn_fwd_pipe_kernel {cfg_name}:"):
+                return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_run(cfg, steps, torch, synth, dev):
+    q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
+    runner = LayerRunner(cfg, q, k, v)
+    for _ in range(steps):
+        runner.step()
+    torch.cuda.synchronize()
+    src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)   # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc run done", flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -272,6 +318,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg = synth.CONFIGS[args.config]
+    if args.pmc_run:
+        pmc_run(cfg, args.steps, torch, synth, dev)
+        return
     t_gen = time.perf_counter()
     q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
     gen_s = time.perf_counter() - t_gen
@@ -318,7 +367,9 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(cfg.name),
+            "traffic_source": "profiles/attn_fwd_c2_traffic.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                              "calibrated by a 1 GiB copy)",
         },
         "gen_s": round(gen_s, 1),
     }

@@ -113,6 +113,25 @@ def test_sparse_gqa_ragged(hip_lib, D, block_m):
     check_close(out, ref, f"D={D} bm={block_m}")
 
 
+def test_repeated_slot_counts_twice(hip_lib):
+    """A block listed twice in a tile's kv_idx is visited twice (the reference
+    kernel's loop, src/triton_block_attn.py:229-259), for every tile shape."""
+    print("[case] repeated slots", flush=True)
+    for D, block_m in ((128, 64), (64, 64), (256, 64), (128, 32)):
+        B, H, Hk, M = 1, 4, 2, 320
+        q, k, v = qkv_small(11 + D, B, H, Hk, M, M, D)
+        qt, nb = (M + block_m - 1) // block_m, M // 64
+        kv = torch.full((B, H, qt, 6), nb, dtype=torch.int32)
+        for t in range(qt):
+            self_blk = min((t * block_m + block_m - 1) // 64, nb - 1)
+            kv[:, :, t, :4] = torch.tensor([0, self_blk, 0, self_blk], dtype=torch.int32)
+        out = block_sparse_attn_v2(q.to(DEV), k.to(DEV), v.to(DEV), kv.to(DEV), D ** -0.5,
+                                   block_m=block_m)
+        ref = OA.gathered_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                    kv.numpy(), D ** -0.5, block_m=block_m)
+        check_close(out, ref, f"dup D={D} bm={block_m}")
+
+
 def test_strided_views_and_repeat_kv_heads(hip_lib):
     """[B, S, H, D] views in and out, and H-head (repeat_kv'd) K/V, give the
     same bits as contiguous GQA inputs."""

@@ -17,12 +17,18 @@
 // row (lane & 15 of each 16-row N-tile) through both products, so the row
 // max / row sum / rescale of the online softmax are lane-local plus two
 // cross-lane steps, and P never leaves registers.  Keys are relabelled
-// inside the 64-key block (pi below) so that each lane's eight P^T values
-// are eight consecutive keys; V is pre-transposed per block ([NB][D][64],
-// v_block_transpose_kernel) so both K and V^T operands are single 16-byte
-// loads straight from global memory into MFMA operand registers.  There is
-// no reuse of a K/V block between the waves of one tile that LDS staging
-// could exploit at 64 rows per wave, so LDS is not used.
+// inside a block so that each lane's eight P^T values are eight consecutive
+// keys, which makes the V^T operand eight consecutive keys of one column.
+//
+// Two kernels share this mapping:
+//   attn_fwd_pipe_kernel  64-row tiles at head_dim 64 / 128 (the default):
+//                         32-key half blocks, S of the next half block
+//                         computed while the softmax of the current one runs,
+//                         K / V^T read from an operand-order copy
+//                         (kv_operand_kernel) two half blocks ahead;
+//   attn_fwd_kernel       head_dim 256 and 32-row tiles: K read in place,
+//                         V^T from a per-block transposed copy
+//                         (v_block_transpose_kernel); launch shape selectable.
 //
 // Launch order: heaviest tiles first (t descending; a tile visits up to
 // min(t + 1, k_slots) blocks), and the G query heads of one (b, KV head, t)
@@ -483,19 +489,47 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   const int row0 = t * BM;
   const int q_last = row0 + BM - 1;
 
-  // ---- visited blocks of this tile, in slot order, compacted into LDS -----
+  // ---- visited blocks of this tile, compacted into LDS in ascending order ---
+  // (the heads of a KV group and neighbouring tiles then sweep shared blocks
+  // together, which keeps them in L2).  A block listed twice in a row keeps
+  // the slot order, so it is visited twice as the reference loop does.
   const int32_t* idx = kv_idx + b * si_b + h * si_h + t * si_t;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t* bits = reinterpret_cast<uint32_t*>(blist + k_slots);
+  const int n_words = (min(t, NB - 1) >> 5) + 1;     // visible blocks are <= t
+  for (int w = lane; w < n_words; w += 64) bits[w] = 0u;
+  wave_lds_sync();
   int nv = 0;
+  bool dup = false;
   for (int base = 0; base < k_slots; base += 64) {
     const int s = base + lane;
     const int blk = s < k_slots ? idx[s] : -1;
     const bool ok = blk >= 0 && blk < NB && blk * kBlock <= q_last;
     const uint64_t bal = __ballot(ok);
-    if (ok) blist[nv + __popcll(bal & lt_mask)] = blk;
+    if (ok) {
+      blist[nv + __popcll(bal & lt_mask)] = blk;
+      const uint32_t bit = 1u << (blk & 31);
+      dup |= (atomicOr(&bits[blk >> 5], bit) & bit) != 0u;
+    }
     nv += __popcll(bal);
   }
   wave_lds_sync();
+  if (__ballot(dup) == 0) {
+    int pos = 0;
+    for (int w0 = 0; w0 < n_words; w0 += 64) {
+      const int w = w0 + lane;
+      uint32_t word = w < n_words ? bits[w] : 0u;
+      const uint32_t cnt = __popc(word);
+      int at = pos + static_cast<int>(wave_excl_scan(cnt, lane));
+      while (word) {
+        const int j = __ffs(word) - 1;
+        blist[at++] = w * 32 + j;
+        word &= word - 1u;
+      }
+      pos = __shfl(at, 63, 64);
+    }
+    wave_lds_sync();
+  }
 
   // ---- Q tile: MFMA B operands held in registers ---------------------------
   const uint16_t* qb = q + b * sq_b + h * sq_h;
@@ -716,7 +750,8 @@ static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h
   const int grp = H / Hk;
   const int units = B * Hk * Qt;
   const int64_t wgs = 8LL * grp * ((units + 7) / 8);
-  attn_fwd_pipe_kernel<D, QLDS><<<dim3(static_cast<unsigned>(wgs)), 64, k_slots * 4, stream>>>(
+  const size_t lds = static_cast<size_t>(k_slots) * 4 + static_cast<size_t>((NB + 31) / 32) * 4;
+  attn_fwd_pipe_kernel<D, QLDS><<<dim3(static_cast<unsigned>(wgs)), 64, lds, stream>>>(
       q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b, si_h, si_t, B, Hk, M, N, NB,
       Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
   return hipGetLastError();

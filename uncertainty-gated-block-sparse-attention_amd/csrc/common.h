@@ -134,6 +134,17 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
+// Exclusive prefix sum across the wavefront.
+__device__ __forceinline__ uint32_t wave_excl_scan(uint32_t x, int lane) {
+  uint32_t incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), off, 64));
+    if (lane >= off) incl += y;
+  }
+  return incl - x;
+}
+
 // Order LDS traffic of one wavefront against itself (no workgroup barrier).
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -49,17 +49,6 @@ __host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP) {
   return s;
 }
 
-// Exclusive prefix sum across the wavefront.
-__device__ __forceinline__ uint32_t wave_excl_scan(uint32_t x, int lane) {
-  uint32_t incl = x;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), off, 64));
-    if (lane >= off) incl += y;
-  }
-  return incl - x;
-}
-
 template <int D, int P, int KP>
 __global__ __launch_bounds__(512) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
