@@ -318,8 +318,8 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 
     // ---- causal / bounds mask, online softmax (log2 domain) -------------
     const bool need_mask = (kbase + kBlock - 1 > row0) || (kbase + kBlock > N);
-    float alpha[NT];
-    bool moved = false;
+    float mx_s[NT];
+    bool grow = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int row = row0 + 16 * nt + r16;
@@ -337,28 +337,33 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[mt][nt][i]);
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      const float m_new = fmaxf(m[nt], mx * scale_log2);
-      moved |= m_new != m[nt];
-      alpha[nt] = __builtin_amdgcn_exp2f(m[nt] - m_new);
-      m[nt] = m_new;
+      mx = quad_rows_max(mx);
+      mx_s[nt] = mx * scale_log2;
+      grow |= mx_s[nt] > m[nt] + kLazyLog2;
+    }
+    if (__ballot(grow)) {      // move the offsets (lazy: rarely after the first blocks)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float m_new = fmaxf(m[nt], mx_s[nt]);
+        const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_new);
+        m[nt] = m_new;
+        l[nt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
       float sum = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], scale_log2, -m_new));
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], scale_log2, -m[nt]));
           st[mt][nt][i] = p;
           sum += p;
         }
-      l[nt] = l[nt] * alpha[nt] + sum;
-    }
-    if (__ballot(moved)) {     // visiting blocks best-first leaves the max mostly unchanged
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) o[dt][nt] *= alpha[nt];
+      l[nt] += sum;
     }
 
     // ---- O^T += V^T . P^T ----------------------------------------------
@@ -387,8 +392,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
   // ---- row sums, cross-wave merge (SPLIT), normalise and store ----------
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    l[nt] += shfl_xor_f(l[nt], 16);
-    l[nt] += shfl_xor_f(l[nt], 32);
+    l[nt] = quad_rows_sum(l[nt]);
   }
   if constexpr (SPLIT) {
     float* part = reinterpret_cast<float*>(smem);
@@ -458,8 +462,8 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 // (K(u+3) is requested after phase 1, V^T(u+2) after phase 2); the two S,
 // K and V register sets alternate between consecutive steps (the loop is
 // unrolled by 2).  Half blocks keep the live set at about 400 VGPRs: O^T
-// 128, two S 64, P 16, Q 64, two K 64, two V^T 64.  The rescale of O by
-// exp2(m_old - m_new) is skipped when no row max moved.  The tile's kv_idx
+// 128, two S 64, P 16, Q 64, two K 64, two V^T 64.  The exp2 offsets are
+// lazy (kLazyLog2), so the rescale of O is skipped on most half blocks.  The tile's kv_idx
 // row is compacted into LDS once (visited blocks only), so sentinel and
 // invisible slots cost nothing in the loop.
 template <int D, bool QLDS>
@@ -553,21 +557,24 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   const uint32_t loff = static_cast<uint32_t>(lane * 16);
   const int nu = 2 * nv;
 
-  auto blk_of = [&](int u) -> int { return __builtin_amdgcn_readfirstlane(blist[u >> 1]); };
   typedef bf16x8 KSet[2][KS];
   typedef bf16x8 VSet[DT];
   typedef f32x4 SBuf[2][NT];
-  auto load_k = [&](int u, KSet& kf) {
-    u = min(u, nu - 1);
-    const uint32_t sb = static_cast<uint32_t>((2 * blk_of(u) + (u & 1)) * 2 * KS * 1024);
+  // Half block u (clamped to the last one) -> its block id (LDS read; the
+  // caller applies readfirstlane where it needs the id, so the read can be
+  // issued early) and its half.
+  auto clamp_u = [&](int u) -> int { return min(u, nu - 1); };
+  auto blk_raw = [&](int u) -> int { return blist[clamp_u(u) >> 1]; };
+  auto uni = [](int x) -> int { return __builtin_amdgcn_readfirstlane(x); };
+  auto load_k = [&](int blk, int half, KSet& kf) {
+    const uint32_t sb = static_cast<uint32_t>((2 * blk + half) * 2 * KS * 1024);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = buffer_load_bf16x8(krs, loff + (mt * KS + ks) * 1024, sb);
   };
-  auto load_v = [&](int u, VSet& vf) {
-    u = min(u, nu - 1);
-    const uint32_t sb = static_cast<uint32_t>((2 * blk_of(u) + (u & 1)) * DT * 1024);
+  auto load_v = [&](int blk, int half, VSet& vf) {
+    const uint32_t sb = static_cast<uint32_t>((2 * blk + half) * DT * 1024);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vf[dt] = buffer_load_bf16x8(vrs, loff + dt * 1024, sb);
   };
@@ -577,25 +584,14 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[NT], l[NT], alpha[NT];
+  float m[NT], l[NT], mx_s[NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; alpha[nt] = 1.f; }
+  for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; mx_s[nt] = -INFINITY; }
+  bf16x8 pb[NT];
 
-  auto qk = [&](SBuf& st, const KSet& kf) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) st[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) st[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], st[mt][nt]);
-  };
   // Causal / bounds mask (only half blocks crossing the diagonal or N).
-  auto mask = [&](SBuf& st, int u) {
-    const int kbase = blk_of(u) * kBlock + 32 * (u & 1);
+  auto mask = [&](SBuf& st, int blk, int half) {
+    const int kbase = blk * kBlock + 32 * half;
     if ((kbase + 31 > row0) || (kbase + 32 > N)) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
@@ -610,33 +606,107 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
       }
     }
   };
-  auto rowmax = [&](const SBuf& st) -> bool {
-    bool moved = false;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[mt][nt][i]);
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
-      const float m_new = fmaxf(m[nt], mx * scale_log2);
-      moved |= m_new != m[nt];
-      alpha[nt] = __builtin_amdgcn_exp2f(m[nt] - m_new);
-      m[nt] = m_new;
-    }
-    return __ballot(moved) != 0;
-  };
+  // Move the exp2 offsets to the new row maxima and rescale l and O.
   auto rescale = [&]() {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      l[nt] *= alpha[nt];
+      const float m_new = fmaxf(m[nt], mx_s[nt]);
+      const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_new);
+      m[nt] = m_new;
+      l[nt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= alpha[nt];
+      for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= alpha;
     }
   };
-  bf16x8 pb[NT];
+  // One unit of the row-max work on S (8 values per lane per N-tile):
+  // stage 0 max of the eight, 1 / 2 the xor-16 / xor-32 lane steps, 3 the
+  // scale and the lazy-offset test.
+  float rm[NT];
+  bool grow = false;
+  auto rowmax_unit = [&](const SBuf& st, int nt, int stage) {
+    if (stage == 0) {
+      rm[nt] = fmaxf(fmaxf(fmaxf(st[0][nt][0], st[0][nt][1]), fmaxf(st[0][nt][2], st[0][nt][3])),
+                     fmaxf(fmaxf(st[1][nt][0], st[1][nt][1]), fmaxf(st[1][nt][2], st[1][nt][3])));
+    } else if (stage == 1) {
+      auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(rm[nt]), __float_as_uint(rm[nt]), false, false);
+      rm[nt] = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    } else if (stage == 2) {
+      auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(rm[nt]), __float_as_uint(rm[nt]), false, false);
+      rm[nt] = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    } else {
+      mx_s[nt] = rm[nt] * scale_log2;
+      grow |= mx_s[nt] > m[nt] + kLazyLog2;
+    }
+  };
+  // S^T of one half block without interleaved work (prologue).
+  auto qk = [&](SBuf& st, const KSet& kf) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          st[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[mt][nt]);
+  };
+
+  // Phase 1, woven by hand (the one wave per SIMD issues in order, so the
+  // VALU work must sit between the MFMAs in the instruction stream): each
+  // pair of S(u+1) MFMAs is followed by the exp2 / row sum / bf16 packing of
+  // PE elements of S(u); sched_barrier keeps the compiler from regrouping.
+  constexpr int NM1 = 2 * NT * KS;                  // MFMAs of S^T per half block
+  constexpr int PE = 8 * NT / (NM1 / 2);            // softmax elements per MFMA pair
+  static_assert(PE * (NM1 / 2) == 8 * NT, "softmax elements must split evenly");
+  auto phase1 = [&](const SBuf& cur, SBuf& nxt, const KSet& kf) {
+    float p[NT][8], sum[NT];
+    uint32_t w[NT][4];
+#pragma unroll
+    for (int j = 0; j < NM1; j += 2) {
+#pragma unroll
+      for (int jj = j; jj < j + 2; ++jj) {
+        const int ks = jj / (2 * NT), mt = (jj / NT) & 1, nt = jj % NT;
+        nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
+      }
+#pragma unroll
+      for (int e = (j / 2) * PE; e < (j / 2 + 1) * PE; ++e) {
+        const int nt = e / 8, kk = e % 8, mt = kk / 4, i = kk % 4;
+        p[nt][kk] = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[mt][nt][i], scale_log2, -m[nt]));
+        sum[nt] = kk == 0 ? p[nt][0] : sum[nt] + p[nt][kk];
+        if (kk & 1) w[nt][kk / 2] = cvt_pk_bf16(p[nt][kk - 1], p[nt][kk]);
+        if (kk == 7) {
+          l[nt] += sum[nt];
+          pb[nt] = __builtin_bit_cast(bf16x8, u32x4{w[nt][0], w[nt][1], w[nt][2], w[nt][3]});
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Phase 2, woven likewise: O^T += V^T . P^T(u) (DT * NT MFMAs) with the
+  // row-max units of S(u+1).
+  constexpr int NM2 = DT * NT;
+  constexpr int RU = 4 * NT / (NM2 / 2);            // row-max units per MFMA pair
+  static_assert(RU * (NM2 / 2) == 4 * NT, "row-max units must split evenly");
+  auto phase2 = [&](const SBuf& nx, const VSet& vf) -> bool {
+    grow = false;
+#pragma unroll
+    for (int j = 0; j < NM2; j += 2) {
+#pragma unroll
+      for (int jj = j; jj < j + 2; ++jj) {
+        const int dt = jj / NT, nt = jj % NT;
+        o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+      }
+#pragma unroll
+      for (int r = (j / 2) * RU; r < (j / 2 + 1) * RU; ++r) rowmax_unit(nx, r / 4, r % 4);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return __ballot(grow) != 0;
+  };
+  auto rowmax = [&](const SBuf& st) -> bool {
+    grow = false;
+#pragma unroll
+    for (int r = 0; r < 4 * NT; ++r) rowmax_unit(st, r / 4, r % 4);
+    return __ballot(grow) != 0;
+  };
+  // Softmax and P.V of the last half block (epilogue, not woven).
   auto softmax = [&](const SBuf& st) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -646,9 +716,9 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
         p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[0][nt][i], scale_log2, -m[nt]));
         p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[1][nt][i], scale_log2, -m[nt]));
       }
-      float sum = 0.f;
+      float sum = p[0];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum += p[i];
+      for (int i = 1; i < 8; ++i) sum += p[i];
       l[nt] += sum;
       pb[nt] = pack_bf16x8(p);
     }
@@ -665,49 +735,34 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   VSet va, vb;
   // Step u: S(u) in cur, K(u+1) in kc, V(u) in vc; K(u+2) / V(u+1) in flight.
   auto step = [&](SBuf& cur, SBuf& nxt, KSet& kc, VSet& vc, int u) {
-    // phase 1: 32 MFMAs of S(u+1) interleaved one by one with the softmax of
-    // S(u) (the compiler otherwise issues the MFMAs back to back and the one
-    // wave on the SIMD waits for the matrix pipe before its VALU work)
-    softmax(cur);
-    qk(nxt, kc);
-    load_k(u + 3, kc);
-    // P(u) is only read by phase 2; pin it here so it is not sunk past the
-    // mask branch into phase 2's region
+    // block ids of K(u+3), the mask of S(u+1) and V(u+2), read from LDS
+    // before phase 1 so that their latency hides behind it
+    const int rk = blk_raw(u + 3), rm1 = blk_raw(u + 1), rv = blk_raw(u + 2);
+    phase1(cur, nxt, kc);
+    load_k(uni(rk), clamp_u(u + 3) & 1, kc);
+    // P(u) and the row sums are only read later; pin them so that their
+    // computation is not sunk past the mask branch into phase 2's region
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       u32x4 pin = __builtin_bit_cast(u32x4, pb[nt]);
-      asm volatile("" : "+v"(pin));
+      asm volatile("" : "+v"(pin), "+v"(l[nt]));
       pb[nt] = __builtin_bit_cast(bf16x8, pin);
     }
-#pragma unroll
-    for (int i = 0; i < 2 * NT * KS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);   // VALU / transcendental
-    }
-    __builtin_amdgcn_sched_group_barrier(0x020, 2 * KS, 0); // K(u+3) loads
-    mask(nxt, u + 1);
-    // phase 2: 32 MFMAs of O += V^T P^T interleaved with the row max of S(u+1)
-    pv(vc);
-    const bool moved = rowmax(nxt);
-    load_v(u + 2, vc);
-#pragma unroll
-    for (int i = 0; i < DT * NT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x020, DT, 0);     // V(u+2) loads
+    mask(nxt, uni(rm1), (u + 1) & 1);
+    const bool moved = phase2(nxt, vc);
+    load_v(uni(rv), clamp_u(u + 2) & 1, vc);
     if (moved) rescale();
   };
 
   if (nv > 0) {
-    load_k(0, ka);
-    load_k(1, kb);
-    load_v(0, va);
-    load_v(1, vb);
+    load_k(uni(blk_raw(0)), 0, ka);
+    load_k(uni(blk_raw(1)), 1, kb);
+    load_v(uni(blk_raw(0)), 0, va);
+    load_v(uni(blk_raw(1)), 1, vb);
     qk(sa, ka);
-    load_k(2, ka);
-    mask(sa, 0);
-    rowmax(sa);
+    load_k(uni(blk_raw(2)), clamp_u(2) & 1, ka);
+    mask(sa, uni(blk_raw(0)), 0);
+    if (rowmax(sa)) rescale();
     // nu = 2 * nv is even: steady steps u = 0 .. nu - 2, then the last half block.
     int u = 0;
     for (; u + 2 <= nu - 2; u += 2) {
@@ -724,8 +779,7 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float lt = l[nt];
-    lt += shfl_xor_f(lt, 16);
-    lt += shfl_xor_f(lt, 32);
+    lt = quad_rows_sum(lt);
     const float inv = lt > 0.f ? 1.0f / lt : 1.0f;
     const int row = row0 + 16 * nt + r16;
     if (row < M) {

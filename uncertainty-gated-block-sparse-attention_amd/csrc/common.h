@@ -25,6 +25,10 @@ constexpr int kWave = 64;
 constexpr int kBlock = 64;          // tokens per KV block (reference BLOCK)
 constexpr float kFMax = 3.40282346638528859812e+38f;
 constexpr float kLog2e = 1.44269504088896340736f;
+// Online softmax with a lazy offset: the exp2 offset of a row only moves when
+// the row max exceeds it by more than this (log2 units), so P <= 2^8 and the
+// O rescale is skipped on most blocks; O / l does not depend on the offset.
+constexpr float kLazyLog2 = 8.0f;
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -132,6 +136,24 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   uint32_t lo = shfl_xor_u(static_cast<uint32_t>(v), m);
   uint32_t hi = shfl_xor_u(static_cast<uint32_t>(v >> 32), m);
   return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Max / sum over the four lanes r, r + 16, r + 32, r + 48 (every lane gets
+// the result).  v_permlane16_swap / v_permlane32_swap exchange 16-lane rows
+// in the VALU, with no LDS round trip: swapping x with itself leaves rows
+// (0, 0, 2, 2) in one half of the pair and (1, 1, 3, 3) in the other, so the
+// element-wise op of the pair is the xor-16 reduction (likewise xor-32).
+__device__ __forceinline__ float quad_rows_max(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_rows_sum(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Exclusive prefix sum across the wavefront.

@@ -151,8 +151,7 @@ __global__ __launch_bounds__(512) void select_kernel(
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i] * scaling);
-        mx = fmaxf(mx, shfl_xor_f(mx, 16));
-        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        mx = quad_rows_max(mx);
         const int blk = c * kChunk + 16 * nt + r16;
         if (g4 == nt && blk < NB) trow[blk] = mx;
       }
