@@ -107,7 +107,8 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
  * Qt = ceil(M / block_m), block_m 64 or 32, sentinel NB skipped; out
  * [B, H, M, D] bf16 with arbitrary strides (head_dim stride 1).  v may be
  * NULL when workspace already holds ugbsa_attn_prepare_kv(k, v, block_m);
- * otherwise the preparation runs first, on the same stream. */
+ * otherwise the preparation runs first, on the same stream.  scale must be
+ * finite and nonzero (UGBSA_EARG otherwise). */
 int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
                    const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                    const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,

@@ -56,6 +56,12 @@ def test_argument_errors_are_reported_without_launch(lib):
                             1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
                             16, 0, 0, 8, 1, 16, None)
     assert rc == -2 and b"stride" in lib.ugbsa_last_error()
+    # a zero or non-finite softmax scale is rejected before any launch
+    for bad in (0.0, float("inf"), float("nan")):
+        rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
+                                1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, bad,
+                                16, 0, 0, 8, 1, 16, None)
+        assert rc == -1 and b"scale" in lib.ugbsa_last_error(), bad
     rc = lib.ugbsa_router(16, 1, 8, 4, _capi.GRAIN_ROW, _capi.ROUTER_QUANTILE, 0.1, 0, 16,
                           4, 8, 16, 16, 16, None, None)
     assert rc == -1 and b"k_quant" in lib.ugbsa_last_error()

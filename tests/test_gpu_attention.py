@@ -132,6 +132,26 @@ def test_repeated_slot_counts_twice(hip_lib):
         check_close(out, ref, f"dup D={D} bm={block_m}")
 
 
+@pytest.mark.parametrize("D,block_m", [(128, 64), (64, 64), (256, 64), (128, 32)])
+def test_score_drift_and_negative_scale(hip_lib, D, block_m):
+    """Row maxima that climb by far more than 2^8 (log2 units) from block to
+    block exercise the lazy softmax offsets (every climb must move them); a
+    negative scale exercises the sign moved onto Q."""
+    print(f"[case] score drift / negative scale D={D} block_m={block_m}", flush=True)
+    B, H, Hk, M = 1, 4, 2, 512
+    q, k, v = qkv_small(21 + D, B, H, Hk, M, M, D)
+    ramp = (1.0 + torch.arange(M) // 64).float()[None, None, :, None]   # x1 .. x8 by block
+    k = (k.float() * ramp).to(torch.bfloat16)
+    keep = torch.ones(B, H, M, M // 64, dtype=torch.bool)
+    kv_idx, _ = _compute_kv_idx(keep, block_m)
+    for scale in (4 * D ** -0.5, -(D ** -0.5)):
+        out = block_sparse_attn_v2(q.to(DEV), k.to(DEV), v.to(DEV), kv_idx.to(DEV), scale,
+                                   block_m=block_m)
+        ref = OA.gathered_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                    kv_idx.numpy(), scale, block_m=block_m)
+        check_close(out, ref, f"drift D={D} bm={block_m} scale={scale:+.3f}")
+
+
 def test_strided_views_and_repeat_kv_heads(hip_lib):
     """[B, S, H, D] views in and out, and H-head (repeat_kv'd) K/V, give the
     same bits as contiguous GQA inputs."""

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
     const uint16_t* __restrict__ vt, const int32_t* __restrict__ kv_idx, int64_t si_b,
     int64_t si_h, int64_t si_t, int B, int Hk, int M, int N, int NB, int Qt, int k_slots,
-    float scale_log2, uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m,
+    float scale_signed, uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m,
     int units, int grp) {
   using S = AttnShape<D, NT, WPT, SPLIT, QLDS, PF>;
   constexpr int BM = S::BM, KS = S::KS, DT = S::DT;
@@ -209,6 +209,10 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
   const int g4 = lane >> 4, r16 = lane & 15;
   const int row0 = t * BM + (SPLIT ? 0 : wave * 16 * NT);
   const uint16_t* qb = q + b * sq_b + h * sq_h;
+  // A negative scale is moved onto Q (bf16 negation is exact), so the
+  // softmax below always scales by scale_log2 > 0.
+  const uint32_t qsign = scale_signed < 0.f ? 0x80008000u : 0u;
+  const float scale_log2 = fabsf(scale_signed);
 
   // ---- Q (B operand of S^T): registers or LDS ---------------------------
   bf16x8 qf[QLDS ? 1 : NT][QLDS ? 1 : KS];
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
       const int r = pi / CH, c = pi % CH;
       const int row = t * BM + r;
       u32x4 val = {0u, 0u, 0u, 0u};
-      if (row < M) val = *reinterpret_cast<const u32x4*>(qb + row * sq_m + c * 8);
+      if (row < M) val = *reinterpret_cast<const u32x4*>(qb + row * sq_m + c * 8) ^ qsign;
       *reinterpret_cast<u32x4*>(qs + r * S::QROW + c * 8) = val;
     }
     __syncthreads();
@@ -229,7 +233,8 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
       const int row = row0 + 16 * nt + r16;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        qf[nt][ks] = row < M ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4) : zero_bf16x8();
+        qf[nt][ks] = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
+                             : zero_bf16x8();
     }
   }
   const int qlds_row0 = (row0 - t * BM) + r16;    // this lane's first row inside the tile
@@ -456,16 +461,18 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 // (online softmax is exact at any key granularity).  Step u overlaps
 //   phase 1  MFMA: S^T(u+1) = K(u+1) . Q^T     ||  VALU: P(u) = exp2(S(u) - m),
 //                                                   row sums, bf16 packing
-//   phase 2  MFMA: O^T += V^T(u) . P^T(u)      ||  VALU: mask + row max of
-//                                                   S(u+1), new m, rescale factor
-// K and V^T operands are prefetched into registers two half blocks ahead
-// (K(u+3) is requested after phase 1, V^T(u+2) after phase 2); the two S,
-// K and V register sets alternate between consecutive steps (the loop is
-// unrolled by 2).  Half blocks keep the live set at about 400 VGPRs: O^T
-// 128, two S 64, P 16, Q 64, two K 64, two V^T 64.  The exp2 offsets are
-// lazy (kLazyLog2), so the rescale of O is skipped on most half blocks.  The tile's kv_idx
-// row is compacted into LDS once (visited blocks only), so sentinel and
-// invisible slots cost nothing in the loop.
+//   phase 2  MFMA: O^T += V^T(u) . P^T(u)      ||  VALU: lane max of S(u+1)
+//                                                   and the lazy-offset test
+// with the VALU work woven between the MFMAs by hand.  The exp2 offsets m
+// are lazy (kLazyLog2) and tested lane-locally; the cross-lane row max and
+// the rescale of l and O run only when an offset must move, which after the
+// first blocks is rare.  K and V^T operands are prefetched into registers
+// two half blocks ahead (K(u+3) is requested after phase 1, V^T(u+2) after
+// phase 2); the two S, K and V register sets alternate between consecutive
+// steps (the loop is unrolled by 2).  Half blocks keep the live set at about
+// 430 registers: O^T 128, two S 64, P 16, Q 64, two K 64, two V^T 64.  The
+// tile's kv_idx row is compacted into LDS once (visited blocks only), so
+// sentinel and invisible slots cost nothing in the loop.
 template <int D, bool QLDS>
 __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
@@ -545,6 +552,16 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
     for (int ks = 0; ks < KS; ++ks)
       qf[nt][ks] = row < M ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4) : zero_bf16x8();
   }
+  // A negative scale is moved onto Q (bf16 negation is exact), so the
+  // scores the softmax sees are always scaled by sl2 > 0.
+  const float sl2 = fabsf(scale_log2);
+  if (scale_log2 < 0.f) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[nt][ks] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, qf[nt][ks]) ^ 0x80008000u);
+  }
 
   // K and V^T operands of this KV head, in load order (kv_operand_kernel):
   // half block (blk, half) = K slabs at ((2 blk + half) * 2 * KS) KiB and
@@ -584,9 +601,9 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[NT], l[NT], mx_s[NT];
+  float m[NT], l[NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; mx_s[nt] = -INFINITY; }
+  for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; }
   bf16x8 pb[NT];
 
   // Causal / bounds mask (only half blocks crossing the diagonal or N).
@@ -606,36 +623,64 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
       }
     }
   };
-  // Move the exp2 offsets to the new row maxima and rescale l and O.
+  // Lazy offsets, tested lane-locally: a row's offset m only moves when some
+  // lane's max of its raw scores exceeds thr = (m + kLazyLog2) / sl2; the
+  // cross-lane row max is only formed inside the (rare) rescale.
+  float thr[NT], rm[NT], tm[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) thr[nt] = -INFINITY;
+  const float inv_sl2 = 1.0f / sl2;
+  // +inf in a register the optimiser cannot see through: med3(a, b, +inf) is
+  // max(a, b) without the canonicalising copies that fmaxf of MFMA results
+  // gets in IEEE mode.
+  float pinf = INFINITY;
+  asm volatile("" : "+v"(pinf));
+  auto mx2 = [&](float a, float b) -> float { return __builtin_amdgcn_fmed3f(a, b, pinf); };
+  bool grow = false;
+  // Row-max unit r of S (nt = r / 4): stages 0-2 the max tree of the lane's
+  // eight values, stage 3 the test against thr.
+  auto rowmax_unit = [&](const SBuf& st, int r) {
+    const int nt = r / 4, stage = r % 4;
+    if (stage == 0) {
+      tm[nt][0] = mx2(st[0][nt][0], st[0][nt][1]);
+      tm[nt][1] = mx2(st[0][nt][2], st[0][nt][3]);
+    } else if (stage == 1) {
+      tm[nt][2] = mx2(st[1][nt][0], st[1][nt][1]);
+      tm[nt][3] = mx2(st[1][nt][2], st[1][nt][3]);
+    } else if (stage == 2) {
+      tm[nt][0] = mx2(tm[nt][0], tm[nt][1]);
+      tm[nt][2] = mx2(tm[nt][2], tm[nt][3]);
+    } else {
+      rm[nt] = mx2(tm[nt][0], tm[nt][2]);
+      grow |= rm[nt] > thr[nt];
+    }
+  };
+  // Move the offsets to the new row maxima (lane maxima rm -> row maxima)
+  // and rescale l and O.
   auto rescale = [&]() {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float m_new = fmaxf(m[nt], mx_s[nt]);
+      const float m_new = fmaxf(m[nt], quad_rows_max(rm[nt]) * sl2);
       const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_new);
       m[nt] = m_new;
+      thr[nt] = (m_new + kLazyLog2) * inv_sl2;
       l[nt] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= alpha;
     }
   };
-  // One unit of the row-max work on S (8 values per lane per N-tile):
-  // stage 0 max of the eight, 1 / 2 the xor-16 / xor-32 lane steps, 3 the
-  // scale and the lazy-offset test.
-  float rm[NT];
-  bool grow = false;
-  auto rowmax_unit = [&](const SBuf& st, int nt, int stage) {
-    if (stage == 0) {
-      rm[nt] = fmaxf(fmaxf(fmaxf(st[0][nt][0], st[0][nt][1]), fmaxf(st[0][nt][2], st[0][nt][3])),
-                     fmaxf(fmaxf(st[1][nt][0], st[1][nt][1]), fmaxf(st[1][nt][2], st[1][nt][3])));
-    } else if (stage == 1) {
-      auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(rm[nt]), __float_as_uint(rm[nt]), false, false);
-      rm[nt] = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    } else if (stage == 2) {
-      auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(rm[nt]), __float_as_uint(rm[nt]), false, false);
-      rm[nt] = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    } else {
-      mx_s[nt] = rm[nt] * scale_log2;
-      grow |= mx_s[nt] > m[nt] + kLazyLog2;
+  // Softmax element e of S (nt = e / 8): P = exp2(S * sl2 - m), the row sum
+  // and the bf16 packing of P into pb.
+  float p[NT][8], sum[NT];
+  uint32_t w[NT][4];
+  auto softmax_elem = [&](const SBuf& st, int e) {
+    const int nt = e / 8, kk = e % 8, mt = kk / 4, i = kk % 4;
+    p[nt][kk] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], sl2, -m[nt]));
+    sum[nt] = kk == 0 ? p[nt][0] : sum[nt] + p[nt][kk];
+    if (kk & 1) w[nt][kk / 2] = cvt_pk_bf16(p[nt][kk - 1], p[nt][kk]);
+    if (kk == 7) {
+      l[nt] += sum[nt];
+      pb[nt] = __builtin_bit_cast(bf16x8, u32x4{w[nt][0], w[nt][1], w[nt][2], w[nt][3]});
     }
   };
   // S^T of one half block without interleaved work (prologue).
@@ -649,53 +694,40 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
           st[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[mt][nt]);
   };
 
-  // Phase 1, woven by hand (the one wave per SIMD issues in order, so the
-  // VALU work must sit between the MFMAs in the instruction stream): each
-  // pair of S(u+1) MFMAs is followed by the exp2 / row sum / bf16 packing of
-  // PE elements of S(u); sched_barrier keeps the compiler from regrouping.
-  constexpr int NM1 = 2 * NT * KS;                  // MFMAs of S^T per half block
-  constexpr int PE = 8 * NT / (NM1 / 2);            // softmax elements per MFMA pair
-  static_assert(PE * (NM1 / 2) == 8 * NT, "softmax elements must split evenly");
+  // The two phases of a step are woven by hand (one wave per SIMD issues in
+  // order, so VALU work has to sit between the MFMAs of the instruction
+  // stream); sched_barrier keeps the compiler from regrouping them.
+  //   phase 1: S^T(u+1) (NM1 MFMAs) || softmax of S(u) (32 elements a lane)
+  //   phase 2: O^T += V^T P^T(u) (NM2 MFMAs) || the row-max test of S(u+1)
+  constexpr int NM1 = 2 * NT * KS, P1 = NM1 / 2;
+  constexpr int EPP = 8 * NT / P1;                  // softmax elements per MFMA pair
+  constexpr int NM2 = DT * NT, P2 = NM2 / 2;
+  constexpr int RPP = 4 * NT / P2;                  // row-max units per MFMA pair
+  static_assert(EPP * P1 == 8 * NT && RPP * P2 == 4 * NT, "phase work must split evenly");
   auto phase1 = [&](const SBuf& cur, SBuf& nxt, const KSet& kf) {
-    float p[NT][8], sum[NT];
-    uint32_t w[NT][4];
 #pragma unroll
-    for (int j = 0; j < NM1; j += 2) {
+    for (int j = 0; j < P1; ++j) {
 #pragma unroll
-      for (int jj = j; jj < j + 2; ++jj) {
+      for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
         const int ks = jj / (2 * NT), mt = (jj / NT) & 1, nt = jj % NT;
         nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
       }
 #pragma unroll
-      for (int e = (j / 2) * PE; e < (j / 2 + 1) * PE; ++e) {
-        const int nt = e / 8, kk = e % 8, mt = kk / 4, i = kk % 4;
-        p[nt][kk] = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[mt][nt][i], scale_log2, -m[nt]));
-        sum[nt] = kk == 0 ? p[nt][0] : sum[nt] + p[nt][kk];
-        if (kk & 1) w[nt][kk / 2] = cvt_pk_bf16(p[nt][kk - 1], p[nt][kk]);
-        if (kk == 7) {
-          l[nt] += sum[nt];
-          pb[nt] = __builtin_bit_cast(bf16x8, u32x4{w[nt][0], w[nt][1], w[nt][2], w[nt][3]});
-        }
-      }
+      for (int e = j * EPP; e < (j + 1) * EPP; ++e) softmax_elem(cur, e);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // Phase 2, woven likewise: O^T += V^T . P^T(u) (DT * NT MFMAs) with the
-  // row-max units of S(u+1).
-  constexpr int NM2 = DT * NT;
-  constexpr int RU = 4 * NT / (NM2 / 2);            // row-max units per MFMA pair
-  static_assert(RU * (NM2 / 2) == 4 * NT, "row-max units must split evenly");
   auto phase2 = [&](const SBuf& nx, const VSet& vf) -> bool {
     grow = false;
 #pragma unroll
-    for (int j = 0; j < NM2; j += 2) {
+    for (int j = 0; j < P2; ++j) {
 #pragma unroll
-      for (int jj = j; jj < j + 2; ++jj) {
+      for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
         const int dt = jj / NT, nt = jj % NT;
         o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
       }
 #pragma unroll
-      for (int r = (j / 2) * RU; r < (j / 2 + 1) * RU; ++r) rowmax_unit(nx, r / 4, r % 4);
+      for (int r = j * RPP; r < (j + 1) * RPP; ++r) rowmax_unit(nx, r);
       __builtin_amdgcn_sched_barrier(0);
     }
     return __ballot(grow) != 0;
@@ -703,25 +735,13 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   auto rowmax = [&](const SBuf& st) -> bool {
     grow = false;
 #pragma unroll
-    for (int r = 0; r < 4 * NT; ++r) rowmax_unit(st, r / 4, r % 4);
+    for (int r = 0; r < 4 * NT; ++r) rowmax_unit(st, r);
     return __ballot(grow) != 0;
   };
   // Softmax and P.V of the last half block (epilogue, not woven).
   auto softmax = [&](const SBuf& st) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float p[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[0][nt][i], scale_log2, -m[nt]));
-        p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[1][nt][i], scale_log2, -m[nt]));
-      }
-      float sum = p[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) sum += p[i];
-      l[nt] += sum;
-      pb[nt] = pack_bf16x8(p);
-    }
+    for (int e = 0; e < 8 * NT; ++e) softmax_elem(st, e);
   };
   auto pv = [&](const VSet& vf) {
 #pragma unroll
@@ -740,8 +760,8 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
     const int rk = blk_raw(u + 3), rm1 = blk_raw(u + 1), rv = blk_raw(u + 2);
     phase1(cur, nxt, kc);
     load_k(uni(rk), clamp_u(u + 3) & 1, kc);
-    // P(u) and the row sums are only read later; pin them so that their
-    // computation is not sunk past the mask branch into phase 2's region
+    // P and the row sums are only read later; pin them so that their
+    // computation is not sunk past the mask branch into phase 2
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       u32x4 pin = __builtin_bit_cast(u32x4, pb[nt]);

@@ -171,6 +171,7 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
   if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
   if (Qt != (M + block_m - 1) / block_m) return fail(UGBSA_EARG, "kv_idx holds %d tiles, M=%d needs %d", Qt, M, (M + block_m - 1) / block_m);
   if (k_slots < 1) return fail(UGBSA_EARG, "k_slots must be positive");
+  if (!(scale != 0.f && scale - scale == 0.f)) return fail(UGBSA_EARG, "scale must be finite and nonzero");
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* vt = static_cast<uint16_t*>(workspace);
   if (static_cast<int64_t>(N) * sk_n * 2 > 0xFFFFFFFFLL || ugbsa_attn_workspace_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
