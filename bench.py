@@ -359,7 +359,8 @@ def main():
                                   / PEAK_BF16_TFLOPS, 4),
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_fwd_kernel",
+            "kernel": (f"attn_fwd_pipe_kernel<{cfg.D}>" if cfg.D in (64, 128)
+                       else f"attn_fwd_kernel<{cfg.D}>"),
             "achieved": round(attn_tflops, 1),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
