@@ -236,6 +236,20 @@ def _block_select_kv_idx_v2(query, key_states, scaling, block_m=64):
     return kv_idx
 
 
+def needle_hit_rate(needle_blocks) -> float:
+    """Mean over logged layers of the fraction of ``needle_blocks`` kept for
+    the last Q tile (union over heads), read from ``SEL.kept_blocks`` as the
+    reference's harness does (src/poc_core.py:77-85).  1.0 when nothing was
+    logged or no needle block is given."""
+    if not SEL.kept_blocks or not needle_blocks:
+        return 1.0
+    rates = []
+    for kept in SEL.kept_blocks.values():
+        hits = sum(1 for b in needle_blocks if b < len(kept) and bool(kept[b]))
+        rates.append(hits / len(needle_blocks))
+    return sum(rates) / len(rates)
+
+
 def block_sparse_attention(module, query, key, value, attention_mask,
                            scaling, dropout=0.0, **kwargs):
     """HF attention function (src/sparse_attention.py:751-788).
