@@ -15,32 +15,36 @@
 //   sigma           (s[k_base-1] - s[k_base]) / max(s[0] - s[k_base], 1e-6) in
 //                   IEEE fp32 (correctly rounded division, denormals kept) (:703-707).
 //
-// Workgroup = one (b, KV head g, Q tile t) and up to 8 of the group's query
-// heads, one wavefront per head.  All waves share each 32-block chunk of the
-// KV head's summary planes, staged once in LDS; each wave computes its
-// 64 x 32 score chunk on MFMA (A = its Q tile from registers, B = planes from
-// LDS), max-pools it over rows in registers and appends 32 tile scores to
-// its LDS row.  The row then goes through a 4-pass 8-bit radix select for
-// the k_slots-th best key, a ballot compaction of the winners (ties at the
-// cut taken in block order) and a register bitonic sort.
+// Workgroup = one (b, KV head g, Q tile t) and W <= 4 of the group's query
+// heads, one wavefront per head (a group of G heads takes ceil(G / 4)
+// workgroups, so two workgroups fit a CU and one's top-k overlaps the
+// other's scoring).  The KV head's summary planes stream through LDS in
+// chunks of CH blocks, double-buffered: chunk c + 1 is fetched into
+// registers while chunk c is scored, then stored to the other buffer, one
+// barrier per chunk.  Each wave computes its 64 x CH score chunk on MFMA
+// (A = its Q tile, with the Quest sign split done once, from registers;
+// B = planes from LDS), max-pools it over rows in registers and appends CH
+// tile scores to its LDS row.  The row then goes through a 4-pass 8-bit radix
+// select for the k_slots-th best key, a ballot compaction of the winners
+// (ties at the cut taken in block order) and a register bitonic sort.
 #include "common.h"
 #include "launch.h"
 
 namespace ugbsa {
 
-constexpr int kChunk = 32;   // KV blocks per LDS chunk
+constexpr int kSelWaves = 8;   // query heads (wavefronts) per workgroup, at most
 
 struct SelectLds {
   int row_stride;      // elements per chunk row (P * D + 8 pad)
-  int chunk_bytes;
+  int chunk_bytes;     // one chunk buffer
   int wave_bytes;
   int trow_off, hist_off, cand_off;  // within a wave's region
 };
 
-__host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP) {
+__host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP, int CH) {
   SelectLds s;
   s.row_stride = P * D + 8;
-  s.chunk_bytes = kChunk * s.row_stride * 2;
+  s.chunk_bytes = CH * s.row_stride * 2;
   const int trow = ((NB * 4) + 15) / 16 * 16;
   s.trow_off = 0;
   s.hist_off = trow;
@@ -49,16 +53,26 @@ __host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP) {
   return s;
 }
 
+// Blocks per LDS chunk: 32 while a block's planes are at most 512 bytes, else 16.
+__host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 256 ? 32 : 16; }
+
 template <int D, int P, int KP>
-__global__ __launch_bounds__(512) void select_kernel(
+__global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
     int W, int n_hc, float scaling, int k_base, int k_slots, int want_sigma,
     int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score) {
   constexpr int KS = D / 32;
   constexpr int R = KP / 64;
+  constexpr int CH = select_chunk(P, D);
+  constexpr int NT = CH / 16;                       // MFMA column tiles per chunk
+  constexpr int PIECES = CH * P * D / 8;            // 16-byte pieces per chunk
+  // pieces a thread prefetches into registers (enough for 4 or more waves;
+  // smaller workgroups copy the rest when the chunk is stored)
+  constexpr int STAGE = (PIECES + 255) / 256;
+  constexpr int QSETS = P == 2 ? 2 : 1;             // Quest: max(q, 0) and min(q, 0)
   extern __shared__ __align__(16) unsigned char smem[];
-  const SelectLds L = select_lds(P, D, NB, KP);
+  const SelectLds L = select_lds(P, D, NB, KP, CH);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -76,8 +90,12 @@ __global__ __launch_bounds__(512) void select_kernel(
   const int h = g * grp + (active ? jh : 0);
   const int H = Hk * grp;
 
-  uint16_t* chunk = reinterpret_cast<uint16_t*>(smem);
-  unsigned char* wreg = smem + L.chunk_bytes + wave * L.wave_bytes;
+  // chunk buffer i at smem + i * chunk_bytes (derived from smem each time, so
+  // the compiler keeps LDS addressing for the operand reads)
+  auto chunk_buf = [&](int i) -> uint16_t* {
+    return reinterpret_cast<uint16_t*>(smem + i * L.chunk_bytes);
+  };
+  unsigned char* wreg = smem + 2 * L.chunk_bytes + wave * L.wave_bytes;
   float* trow = reinterpret_cast<float*>(wreg + L.trow_off);
   uint32_t* hist = reinterpret_cast<uint32_t*>(wreg + L.hist_off);
   uint64_t* cand = reinterpret_cast<uint64_t*>(wreg + L.cand_off);
@@ -85,77 +103,116 @@ __global__ __launch_bounds__(512) void select_kernel(
   const int last_row = min(t * kBlock + kBlock - 1, N - 1);
   const int n_vis = last_row / kBlock + 1;           // blocks 0 .. self(t)
 
-  // Q tile rows as MFMA A operands (zero rows past M, as F.pad in the reference)
-  bf16x8 qf[4][KS];
+  // Q tile rows as MFMA A operands (zero rows past M, as F.pad in the
+  // reference); Quest keeps (max(q, 0), min(q, 0)), which multiply the
+  // K-max and K-min planes.
+  bf16x8 qf[QSETS][4][KS];
   {
     const uint16_t* qb = q + b * sq_b + h * sq_h;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int row = t * kBlock + 16 * mt + r16;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        qf[mt][ks] = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
-                                         : zero_bf16x8();
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 x = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
+                                             : zero_bf16x8();
+        if constexpr (P == 2) {
+          qf[0][mt][ks] = bf16_pos(x);
+          qf[QSETS - 1][mt][ks] = bf16_neg(x);
+        } else {
+          qf[0][mt][ks] = x;
+        }
+      }
     }
   }
 
   const uint16_t* pl = planes + (static_cast<int64_t>(b) * Hk + g) * NB * P * D;
-  const int pieces_per_blk = P * D / 8;
-  const int n_chunks = (n_vis + kChunk - 1) / kChunk;
-  for (int c = 0; c < n_chunks; ++c) {
-    __syncthreads();
-    for (int pi = threadIdx.x; pi < kChunk * pieces_per_blk; pi += nthreads) {
+  constexpr int pieces_per_blk = P * D / 8;
+  const int n_chunks = (n_vis + CH - 1) / CH;
+  u32x4 stage[STAGE];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < STAGE; ++j) {
+      const int pi = threadIdx.x + j * nthreads;
       const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
-      const int blk = c * kChunk + bl;
+      const int blk = c * CH + bl;
+      stage[j] = u32x4{0u, 0u, 0u, 0u};
+      if (pi < PIECES && blk < NB)
+        stage[j] = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
+    }
+  };
+  auto store = [&](int buf, int c) {
+#pragma unroll
+    for (int j = 0; j < STAGE; ++j) {
+      const int pi = threadIdx.x + j * nthreads;
+      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
+      if (pi < PIECES) *reinterpret_cast<u32x4*>(chunk_buf(buf) + bl * L.row_stride + off * 8) = stage[j];
+    }
+    for (int pi = threadIdx.x + STAGE * nthreads; pi < PIECES; pi += nthreads) {
+      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
+      const int blk = c * CH + bl;
       u32x4 v = {0u, 0u, 0u, 0u};
       if (blk < NB) v = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
-      *reinterpret_cast<u32x4*>(chunk + bl * L.row_stride + off * 8) = v;
+      *reinterpret_cast<u32x4*>(chunk_buf(buf) + bl * L.row_stride + off * 8) = v;
     }
-    __syncthreads();
+  };
+  const bool pos_scale = scaling >= 0.f;
+
+  fetch(0);
+  store(0, 0);
+  __syncthreads();
+  for (int c = 0; c < n_chunks; ++c) {
+    const bool more = c + 1 < n_chunks;
+    if (more) fetch(c + 1);
     if (active) {
-      f32x4 acc[4][2];
+      const uint16_t* chunk = chunk_buf(c & 1);
+      f32x4 acc[4][NT];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < P; ++p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          bf16x8 bfr[2];
+          bf16x8 bfr[NT];
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
+          for (int nt = 0; nt < NT; ++nt)
             bfr[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
                                                        p * D + 32 * ks + 8 * g4);
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt) {
-            bf16x8 a = qf[mt][ks];
-            if (P == 2) {
-              // keep the sign split inside the loop (hoisting both halves of
-              // every Q fragment out of the chunk loop doubles their registers)
-              u32x4 raw = __builtin_bit_cast(u32x4, a);
-              asm volatile("" : "+v"(raw));
-              a = __builtin_bit_cast(bf16x8, raw);
-              a = (p == 0) ? bf16_pos(a) : bf16_neg(a);
-            }
+            const bf16x8 a = qf[P == 2 ? p : 0][mt][ks];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma16x16x32(a, bfr[nt], acc[mt][nt]);
+            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma16x16x32(a, bfr[nt], acc[mt][nt]);
           }
         }
       }
-      // tile max over the 64 rows: 16 in-lane values, then across the 4 lane groups
+      // tile max over the 64 rows of (score * scaling): the max (min for a
+      // negative scaling) of the raw sums, scaled once — fl(x * s) is
+      // monotone in x, so this is the max of the scaled scores exactly.
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        float mx = -INFINITY;
+      for (int nt = 0; nt < NT; ++nt) {
+        float mx = acc[0][nt][0];
+        if (pos_scale) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+          for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i] * scaling);
-        mx = quad_rows_max(mx);
-        const int blk = c * kChunk + 16 * nt + r16;
-        if (g4 == nt && blk < NB) trow[blk] = mx;
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i]);
+          mx = quad_rows_max(mx);
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fminf(mx, acc[mt][nt][i]);
+          mx = -quad_rows_max(-mx);
+        }
+        const int blk = c * CH + 16 * nt + r16;
+        if (g4 == nt % 4 && blk < NB) trow[blk] = mx * scaling;
       }
     }
+    if (more) store((c + 1) & 1, c + 1);
+    __syncthreads();
   }
   if (!active) return;   // no workgroup barrier follows
   wave_lds_sync();
@@ -302,13 +359,30 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   const int NB = (N + kBlock - 1) / kBlock;
   const int Qt = (M + kBlock - 1) / kBlock;
   const int grp = H / Hk;
-  const SelectLds L = select_lds(P, D, NB, KP);
+  const SelectLds L = select_lds(P, D, NB, KP, select_chunk(P, D));
   constexpr int kLdsMax = 160 * 1024;
-  int W = grp < 8 ? grp : 8;
-  while (W > 1 && L.chunk_bytes + W * L.wave_bytes > kLdsMax) --W;
-  if (L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
-  const int n_hc = (grp + W - 1) / W;
-  const size_t lds = L.chunk_bytes + static_cast<size_t>(W) * L.wave_bytes;
+  // W heads per workgroup (ceil(grp / W) workgroups per group): the W that
+  // keeps the most active wavefronts on a CU, given its LDS and at most 8
+  // resident waves (about 230 VGPRs each), counting 10 % more when two or
+  // more workgroups share the CU (one's top-k then overlaps another's
+  // scoring); ties go to the larger W, which stages each plane chunk for
+  // more heads.  W < min(grp, 4) counts half: such workgroups cannot
+  // prefetch a whole chunk into registers (they are only chosen when a long
+  // key range leaves no room in LDS for more heads).
+  int W = 0, n_hc = 0;
+  double best = -1.0;
+  for (int w = 1; w <= (grp < kSelWaves ? grp : kSelWaves); ++w) {
+    const size_t lds_w = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(w) * L.wave_bytes;
+    if (lds_w > static_cast<size_t>(kLdsMax)) break;
+    const int hc = (grp + w - 1) / w;
+    int per_cu = static_cast<int>(kLdsMax / lds_w);
+    if (per_cu > 8 / w) per_cu = 8 / w;
+    const double active = per_cu * static_cast<double>(grp) / hc * (per_cu >= 2 ? 1.1 : 1.0) *
+                          (w < (grp < 4 ? grp : 4) ? 0.5 : 1.0);
+    if (active >= best) { best = active; W = w; n_hc = hc; }
+  }
+  if (W == 0 || 2 * L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
+  const size_t lds = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(W) * L.wave_bytes;
   const int64_t wgs = static_cast<int64_t>(B) * Hk * Qt * n_hc;
   auto kern = select_kernel<D, P, KP>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
