@@ -569,9 +569,7 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   const int64_t head_elems = static_cast<int64_t>(NB) * kBlock * D;
   const int64_t part = static_cast<int64_t>(B) * Hk * head_elems;
   const uint16_t* kop_head = vt + (static_cast<int64_t>(b) * Hk + g) * head_elems;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kop_head, static_cast<uint32_t>(head_elems * 2));
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(kop_head + part, static_cast<uint32_t>(head_elems * 2));
-  const uint32_t loff = static_cast<uint32_t>(lane * 16);
+  const uint16_t* vop_head = kop_head + part;
   const int nu = 2 * nv;
 
   typedef bf16x8 KSet[2][KS];
@@ -583,17 +581,20 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   auto clamp_u = [&](int u) -> int { return min(u, nu - 1); };
   auto blk_raw = [&](int u) -> int { return blist[clamp_u(u) >> 1]; };
   auto uni = [](int x) -> int { return __builtin_amdgcn_readfirstlane(x); };
+  // Global (not buffer) loads: a wavefront streams K/V through the vector
+  // memory pipeline faster with them, and every visited block lies inside
+  // the operand copy, so no range check is needed.
   auto load_k = [&](int blk, int half, KSet& kf) {
-    const uint32_t sb = static_cast<uint32_t>((2 * blk + half) * 2 * KS * 1024);
+    const uint16_t* p = kop_head + static_cast<int64_t>(2 * blk + half) * (2 * KS * 512) + lane * 8;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = buffer_load_bf16x8(krs, loff + (mt * KS + ks) * 1024, sb);
+      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = load_bf16x8(p + (mt * KS + ks) * 512);
   };
   auto load_v = [&](int blk, int half, VSet& vf) {
-    const uint32_t sb = static_cast<uint32_t>((2 * blk + half) * DT * 1024);
+    const uint16_t* p = vop_head + static_cast<int64_t>(2 * blk + half) * (DT * 512) + lane * 8;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) vf[dt] = buffer_load_bf16x8(vrs, loff + dt * 1024, sb);
+    for (int dt = 0; dt < DT; ++dt) vf[dt] = load_bf16x8(p + dt * 512);
   };
 
   f32x4 o[DT][NT];

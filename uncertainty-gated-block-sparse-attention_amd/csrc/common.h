@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace ugbsa {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
@@ -125,6 +127,18 @@ __device__ __forceinline__ float key_float(uint32_t k) {
   return __uint_as_float(u);
 }
 
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0 .. N - 1,
+// so every index the body derives from I is a constant expression (array
+// subscripts stay in registers whatever the loop body's size).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // Cross-lane helpers within one wavefront.
 __device__ __forceinline__ float shfl_xor_f(float v, int m) {
   return __shfl_xor(v, m, kWave);
@@ -154,6 +168,58 @@ __device__ __forceinline__ float quad_rows_sum(float v) {
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// x of lane (lane ^ M) for a compile-time M, in VALU registers (no LDS
+// crossbar): quad_perm for 1 and 2, row_ror 12 / 4 (lane gets lane + 4 /
+// lane - 4 within its 16-lane row) for 4, row_ror 8 for 8, and the halves of
+// v_permlane16_swap / v_permlane32_swap of x with itself (rows (0, 0, 2, 2) /
+// (1, 1, 3, 3), halves (0, 0) / (1, 1)) for 16 and 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lanes(uint32_t x, int lane) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane mask");
+  const int v = static_cast<int>(x);
+  if constexpr (M == 1) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));
+  } else if constexpr (M == 2) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));
+  } else if constexpr (M == 4) {
+    const int down = __builtin_amdgcn_update_dpp(v, v, 0x124, 0xF, 0xF, false);
+    const int up = __builtin_amdgcn_update_dpp(v, v, 0x12C, 0xF, 0xF, false);
+    return static_cast<uint32_t>((lane & 4) ? down : up);
+  } else if constexpr (M == 8) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false));
+  } else if constexpr (M == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? p[0] : p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? p[0] : p[1];
+  }
+}
+template <int M>
+__device__ __forceinline__ uint64_t xor_lanes_u64(uint64_t x, int lane) {
+  const uint32_t lo = xor_lanes<M>(static_cast<uint32_t>(x), lane);
+  const uint32_t hi = xor_lanes<M>(static_cast<uint32_t>(x >> 32), lane);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Bitwise AND / OR across the wavefront (every lane gets the result).
+__device__ __forceinline__ uint32_t wave_and_u32(uint32_t x, int lane) {
+  x &= xor_lanes<32>(x, lane);
+  x &= xor_lanes<16>(x, lane);
+  x &= xor_lanes<8>(x, lane);
+  x &= xor_lanes<4>(x, lane);
+  x &= xor_lanes<2>(x, lane);
+  return x & xor_lanes<1>(x, lane);
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t x, int lane) {
+  x |= xor_lanes<32>(x, lane);
+  x |= xor_lanes<16>(x, lane);
+  x |= xor_lanes<8>(x, lane);
+  x |= xor_lanes<4>(x, lane);
+  x |= xor_lanes<2>(x, lane);
+  return x | xor_lanes<1>(x, lane);
 }
 
 // Exclusive prefix sum across the wavefront.

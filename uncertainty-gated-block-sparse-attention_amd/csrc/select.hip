@@ -53,6 +53,39 @@ __host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP, in
   return s;
 }
 
+// Visible blocks whose keys the top-k keeps in registers (64 per lane step);
+// longer rows run the same radix select on their LDS row.
+constexpr int kRegKeys = 32;
+
+// One radix-select step: hist holds 256 digit counts of the keys still in
+// play; returns the digit of the remaining-th largest key and leaves in
+// remaining its rank among the keys with that digit.
+__device__ __forceinline__ int radix_digit(const uint32_t* hist, int lane, int& remaining,
+                                           int& bin_count) {
+  // lane L holds bins 255-4L .. 252-4L (descending digit order)
+  uint32_t cnt[4], s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { cnt[j] = hist[255 - 4 * lane - j]; s += cnt[j]; }
+  uint32_t cg = wave_excl_scan(s, lane);   // keys in strictly greater digits
+  int found = -1;
+  uint32_t rem_new = 0, fcnt = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (found < 0 && cg < static_cast<uint32_t>(remaining) &&
+        static_cast<uint32_t>(remaining) <= cg + cnt[j]) {
+      found = 255 - 4 * lane - j;
+      rem_new = remaining - cg;
+      fcnt = cnt[j];
+    }
+    cg += cnt[j];
+  }
+  const uint64_t who = __ballot(found >= 0);
+  const int src = __ffsll(static_cast<long long>(who)) - 1;
+  remaining = __shfl(static_cast<int>(rem_new), src, 64);
+  bin_count = __shfl(static_cast<int>(fcnt), src, 64);
+  return __shfl(found, src, 64);
+}
+
 // Blocks per LDS chunk: 32 while a block's planes are at most 512 bytes, else 16.
 __host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 256 ? 32 : 16; }
 
@@ -233,8 +266,105 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   const int n_sel = min(n_vis, K);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   if (n_vis > K) {
+    // Radix select of the K-th largest key tau (8-bit digits from the most
+    // significant), then the keys > tau and the first (K - #greater) keys
+    // == tau in block order are compacted into cand.
     uint32_t prefix = 0, pmask = 0;
     int remaining = K;
+    bool fast = false;
+    if (n_vis <= 64 * kRegKeys) {
+      // Rows of up to 64 * kRegKeys blocks: keys in registers.  The digits
+      // start below the bits that every score except the two forced ones
+      // shares (their AND / OR over the wavefront), so the first pass
+      // spreads the scores over the bins instead of piling them into the
+      // few that the exponent leaves.
+      const int jmax = (n_vis + 63) / 64;
+      uint32_t key[kRegKeys];
+      uint32_t kand = 0xFFFFFFFFu, kor = 0u;
+      static_for<kRegKeys>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        key[j] = 0u;
+        if (j < jmax) {
+          const int i = lane + 64 * j;
+          if (i < n_vis) {
+            key[j] = float_key(trow[i]);
+            if (i != 0 && i != n_vis - 1) { kand &= key[j]; kor |= key[j]; }
+          }
+        }
+      });
+      kand = wave_and_u32(kand, lane);
+      kor = wave_or_u32(kor, lane);
+      const uint32_t diff = kand ^ kor;
+      const int common = diff ? __clz(static_cast<int>(diff)) : 32;
+      pmask = common ? (0xFFFFFFFFu << (32 - common)) : 0u;
+      prefix = kand & pmask;
+      // keys outside the common prefix (the forced ones, and any score that
+      // does not share it): above or below the whole prefix range
+      int above = 0, below = 0;
+      static_for<kRegKeys>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (j < jmax) {
+          const bool valid = lane + 64 * j < n_vis;
+          const uint32_t kp = key[j] & pmask;
+          above += __popcll(__ballot(valid && kp > prefix));
+          below += __popcll(__ballot(valid && kp < prefix));
+        }
+      });
+      remaining = K - above;
+      fast = remaining > 0 && remaining <= n_vis - above - below;
+      if (fast) {
+        for (int shift = 32 - common; shift > 0;) {
+          const int d = shift < 8 ? shift : 8;
+          shift -= d;
+          const uint32_t dmask = (1u << d) - 1u;
+          for (int i = lane; i < 256; i += 64) hist[i] = 0;
+          wave_lds_sync();
+          static_for<kRegKeys>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if (j < jmax && lane + 64 * j < n_vis && (key[j] & pmask) == prefix)
+              atomicAdd(&hist[(key[j] >> shift) & dmask], 1u);
+          });
+          wave_lds_sync();
+          int bin_count;
+          const int digit = radix_digit(hist, lane, remaining, bin_count);
+          prefix |= static_cast<uint32_t>(digit) << shift;
+          pmask |= dmask << shift;
+          wave_lds_sync();
+          // every key with this prefix is selected: the lower digits do
+          // not matter (the sort below orders the selection exactly)
+          if (remaining == bin_count) break;
+        }
+        const int need_eq = remaining;
+        const int n_gt = K - need_eq;
+        int cnt_gt = 0, cnt_eq = 0;
+        static_for<kRegKeys>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          if (j < jmax) {
+            const int i = lane + 64 * j;
+            const uint32_t kp = key[j] & pmask;
+            const bool gt = i < n_vis && kp > prefix;
+            const bool eq = i < n_vis && kp == prefix;
+            const uint64_t bg = __ballot(gt), be = __ballot(eq);
+            const uint64_t comp = (static_cast<uint64_t>(key[j]) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
+            if (gt) {
+              const int pos = cnt_gt + __popcll(bg & lt_mask);
+              if (pos < n_gt) cand[pos] = comp;
+            }
+            if (eq) {
+              const int pos = cnt_eq + __popcll(be & lt_mask);
+              if (pos < need_eq) cand[n_gt + pos] = comp;
+            }
+            cnt_gt += __popcll(bg);
+            cnt_eq += __popcll(be);
+          }
+        });
+      } else {
+        prefix = 0;
+        pmask = 0;
+        remaining = K;
+      }
+    }
+    if (!fast) {
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = lane; i < 256; i += 64) hist[i] = 0;
       wave_lds_sync();
@@ -243,26 +373,8 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
         if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
       wave_lds_sync();
-      // lane L holds bins 255-4L .. 252-4L (descending digit order)
-      uint32_t cnt[4], s = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { cnt[j] = hist[255 - 4 * lane - j]; s += cnt[j]; }
-      uint32_t cg = wave_excl_scan(s, lane);   // keys in strictly greater digits
-      int found = -1;
-      uint32_t rem_new = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (found < 0 && cg < static_cast<uint32_t>(remaining) &&
-            static_cast<uint32_t>(remaining) <= cg + cnt[j]) {
-          found = 255 - 4 * lane - j;
-          rem_new = remaining - cg;
-        }
-        cg += cnt[j];
-      }
-      const uint64_t who = __ballot(found >= 0);
-      const int src = __ffsll(static_cast<long long>(who)) - 1;
-      const int digit = __shfl(found, src, 64);
-      remaining = __shfl(static_cast<int>(rem_new), src, 64);
+      int bin_count;
+      const int digit = radix_digit(hist, lane, remaining, bin_count);
       prefix |= static_cast<uint32_t>(digit) << shift;
       pmask |= 0xFFu << shift;
       wave_lds_sync();
@@ -289,6 +401,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       cnt_gt += __popcll(bg);
       cnt_eq += __popcll(be);
     }
+    }
   } else {
     for (int i = lane; i < n_vis; i += 64)
       cand[i] = (static_cast<uint64_t>(float_key(trow[i])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
@@ -301,27 +414,30 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const int e = lane + 64 * r;
     v[r] = e < n_sel ? cand[e] : 0ull;
   }
-  // bitonic sort, descending
-#pragma unroll
-  for (int kk = 2; kk <= KP; kk <<= 1) {
-#pragma unroll
-    for (int j = kk >> 1; j > 0; j >>= 1) {
+  // bitonic sort, descending: stage (kk, j) compares element e with e ^ j,
+  // across registers for j >= 64, across lanes (register shuffles) below
+  constexpr int LOG_KP = KP == 64 ? 6 : KP == 128 ? 7 : KP == 256 ? 8 : 9;
+  static_assert((1 << LOG_KP) == KP, "KP is a power of two");
+  static_for<LOG_KP>([&](auto lk) {
+    constexpr int kk = 2 << decltype(lk)::value;
+    static_for<decltype(lk)::value + 1>([&](auto lj) {
+      constexpr int j = (kk >> 1) >> decltype(lj)::value;
       uint64_t nv[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int e = lane + 64 * r;
-        const uint64_t other = (j >= 64) ? v[r ^ (j >> 6)] : shfl_xor_u64(v[r], j);
+        uint64_t other;
+        if constexpr (j >= 64) other = v[r ^ (j >> 6)];
+        else other = xor_lanes_u64<j>(v[r], lane);
         const bool lower = (e & j) == 0;
         const bool desc = (e & kk) == 0;
         const bool keep_max = lower == desc;
-        const uint64_t mx = v[r] > other ? v[r] : other;
-        const uint64_t mn = v[r] > other ? other : v[r];
-        nv[r] = keep_max ? mx : mn;
+        nv[r] = (keep_max == (v[r] > other)) ? v[r] : other;
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) v[r] = nv[r];
-    }
-  }
+    });
+  });
 
   int32_t* out = kv_idx + row_id * K;
 #pragma unroll
