@@ -16,6 +16,7 @@
 
 #include <utility>
 
+
 namespace ugbsa {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
