@@ -76,6 +76,30 @@ int ugbsa_select(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_
                  int mode, float scaling, int k_base, int k_slots, int block_m, int32_t* kv_idx,
                  float* sigma, float* tile_score, void* stream);
 
+/* Score dump — the per-tile order statistics and per-head score-noise
+ * estimate that src/dump_block_scores.py (_record, :104-207) records beside
+ * each selection call, computed from kernel 1's planes by kernel 2 in dump
+ * mode plus one reduction kernel.  With s(0) >= s(1) >= ... the tile's
+ * scores before sink/self forcing (invisible blocks -inf, :137-147, sorted
+ * :161; the gaps :162-171):
+ *   g [B, H, Qt]      s(k_b - 1) - s(k_b)
+ *   r [B, H, Qt]      max(s(0) - s(k_b), 1e-9)
+ *   sigma [B, H, Qt]  min(max(g / r, 0), 2), NaN kept
+ *   g_rho [B, H, Qt]  s(rho_k - 1) - s(rho_k)
+ *   valid [Qt] uint8  visible blocks of tile t > rho_k
+ *   tau_hat [B, H]    sqrt(max(0, mean over n_pairs = min(1024, M - 1) row
+ *                     pairs (i, i + 1), i = min(p * max(1, (M - 1) / n_pairs),
+ *                     M - 2), and all NB blocks of (S[i + 1] - S[i])^2 / 2)),
+ *                     S the per-row block score; 0 when M < 2 (:181-194)
+ *   tile_score        optional [B, H, Qt, NB] fp32, the unforced scores.
+ * The caller passes k_b = min(2 * budget_blocks, NB), rho_k = min(2 * k_b,
+ * NB) (:150-151); needs 1 <= k_b < rho_k < NB and rho_k < 512. */
+int ugbsa_score_dump(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                     const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                     int mode, float scaling, int k_b, int rho_k, float* g, float* r,
+                     float* sigma, float* g_rho, uint8_t* valid, float* tau_hat,
+                     float* tile_score, void* stream);
+
 /* Router — row/cell grain, quantile/abs trigger and sentinel emission.
  * Replaces src/sparse_attention.py:708-725.  k_quant = max(1, int(q * B*H*Qt))
  * computed by the caller as the reference does (:714).  Writes sigma_eff

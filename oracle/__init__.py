@@ -15,6 +15,8 @@ Modules
                visibility + sink/self forcing, top-k, sigma margin, router
                (row/cell grain, quantile/abs) and sentinel emission —
                ``src/sparse_attention.py:588-748`` of the reference.
+``score_dump`` order statistics and score-noise estimate of the reference's
+               score-dump diagnostic (``src/dump_block_scores.py:104-207``).
 ``attention``  block-sparse attention over ``kv_idx`` (kernel semantics of
                ``src/triton_block_attn.py:184-264``), the masked dense
                formulation of ``reference_attn`` (``:301-312``) and
@@ -24,4 +26,4 @@ How each function is pinned (beyond restating the reference) is listed in the
 module docstrings; the tests under ``tests/test_oracle_*.py`` hold the checks.
 """
 
-from . import selector, attention  # noqa: F401
+from . import selector, attention, score_dump  # noqa: F401

@@ -112,12 +112,14 @@ def tile_visibility(q_tiles: int, n_keys: int, n_blocks: int,
 
 
 def tile_scores(q, k, scaling: float, use_quest: bool, block_m: int = 64,
-                block_n: int = BLOCK, row_chunk: int = 8192):
+                block_n: int = BLOCK, row_chunk: int = 8192, force: bool = True):
     """tile_score [B, H, Qt, NB] fp32 exactly as handed to ``topk``.
 
     Steps of src/sparse_attention.py: Q zero-pad (:623-625), per-row score
     (:638-648), tile max over rows (:655-656), -inf outside tile visibility
     (:660-666), FMAX on the sink and the tile's self block (:675-681).
+    ``force=False`` stops before the forcing: the scores the score-dump
+    diagnostic ranks (src/dump_block_scores.py:137-147).
     ``k`` may hold H heads (repeat_kv'd, as the reference passes) or Hk heads
     with H % Hk == 0 (query head h reads key head h // (H // Hk), the mapping
     of transformers' ``repeat_kv``).
@@ -151,9 +153,38 @@ def tile_scores(q, k, scaling: float, use_quest: bool, block_m: int = 64,
                     s.reshape(-1, block_m, nb).max(axis=1))
     visible, self_blk = tile_visibility(qt, N, nb, block_m, block_n)
     T[:, :, ~visible] = -np.inf
-    T[..., 0] = FMAX
-    T[:, :, np.arange(qt), self_blk] = FMAX
+    if force:
+        T[..., 0] = FMAX
+        T[:, :, np.arange(qt), self_blk] = FMAX
     return T
+
+
+def row_scores(q, k, scaling: float, use_quest: bool, rows, block_n: int = BLOCK):
+    """Per-row block scores S [B, H, len(rows), NB] fp32 of the given query rows.
+
+    The score of src/sparse_attention.py:638-648 (no tile max, no mask), as
+    the score dump reads it for its noise estimate (src/dump_block_scores.py:
+    126-135, 181-187).
+    """
+    q = _f32(q)
+    B, H, M, D = q.shape
+    Hk = k.shape[1]
+    grp = H // Hk
+    summ = block_summaries(k, use_quest, block_n)
+    sc = np.float32(scaling)
+    rows = np.asarray(rows, dtype=np.int64)
+    nb = (summ[0] if use_quest else summ).shape[2]
+    S = np.empty((B, H, rows.size, nb), np.float32)
+    for b in range(B):
+        for h in range(H):
+            x = q[b, h, rows]
+            if use_quest:
+                kmin, kmax = summ[0][b, h // grp], summ[1][b, h // grp]
+                S[b, h] = (np.maximum(x, np.float32(0)) @ kmax.T
+                           + np.minimum(x, np.float32(0)) @ kmin.T) * sc
+            else:
+                S[b, h] = (x @ summ[b, h // grp].T) * sc
+    return S
 
 
 def sortable_key(x) -> np.ndarray:

@@ -67,3 +67,7 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"k_quant" in lib.ugbsa_last_error()
     with pytest.raises(AssertionError):
         _capi.check(rc, "router")
+    # score dump: rho_k must stay below NB (the reference indexes s(rho_k))
+    rc = lib.ugbsa_score_dump(16, 0, 0, 8, 1, 16, 1, 8, 2, 256, 256, 128, _capi.DTYPE_BF16,
+                              _capi.MODE_QUEST, 0.1, 2, 4, 16, 16, 16, 16, 16, 16, None, None)
+    assert rc == -1 and b"rho_k" in lib.ugbsa_last_error()

@@ -35,6 +35,8 @@ SIGNATURES = {
     "ugbsa_block_summary": (_i, [_p, _i64, _i64, _i64, _i64, _i, _i, _i, _i, _i, _i, _p, _p]),
     "ugbsa_select": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _i, _i,
                           _f, _i, _i, _i, _p, _p, _p, _p]),
+    "ugbsa_score_dump": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _i, _i,
+                              _f, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p]),
     "ugbsa_router": (_i, [_p, _i, _i, _i, _i, _i, _f, _i64, _p, _i, _i, _i, _p, _p, _p, _p]),
     "ugbsa_attn_workspace_elems": (_i64, [_i, _i, _i, _i]),
     "ugbsa_attn_prepare_kv": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64,

@@ -110,6 +110,46 @@ int ugbsa_select(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_
                     "select");
 }
 
+int ugbsa_score_dump(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                     const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                     int mode, float scaling, int k_b, int rho_k, float* g, float* r,
+                     float* sigma, float* g_rho, uint8_t* valid, float* tau_hat,
+                     float* tile_score, void* stream) {
+  int rc = check_dims(B, H, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
+  if (M < 1 || N < 1) return fail(UGBSA_EARG, "M and N must be positive");
+  if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
+  if (planes == nullptr) return fail(UGBSA_EARG, "planes is null");
+  if (!aligned16(planes)) return fail(UGBSA_ELAYOUT, "planes must be 16-byte aligned");
+  if (g == nullptr || r == nullptr || sigma == nullptr || g_rho == nullptr || valid == nullptr ||
+      tau_hat == nullptr)
+    return fail(UGBSA_EARG, "g / r / sigma / g_rho / valid / tau_hat is null");
+  const int nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  if (nb > ugbsa::kMaxBlocksSelect) return fail(UGBSA_EARG, "N=%d gives %d key blocks; the selector holds at most %d", N, nb, ugbsa::kMaxBlocksSelect);
+  if (k_b < 1 || k_b >= rho_k || rho_k >= nb || rho_k + 1 > ugbsa::kMaxSlots)
+    return fail(UGBSA_EARG, "score dump needs 1 <= k_b < rho_k < min(NB=%d, %d) (k_b=%d, rho_k=%d)",
+                nb, ugbsa::kMaxSlots, k_b, rho_k);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  ugbsa::SelectDump dump;
+  dump.g = g;
+  dump.r = r;
+  dump.sigma = sigma;
+  dump.g_rho = g_rho;
+  dump.valid = valid;
+  dump.k_b = k_b;
+  dump.rho_k = rho_k;
+  dump.on = 1;
+  const uint16_t* q16 = static_cast<const uint16_t*>(q);
+  const uint16_t* p16 = static_cast<const uint16_t*>(planes);
+  hipError_t e = ugbsa::launch_select(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, mode, scaling,
+                                      k_b, rho_k + 1, 0, nullptr, nullptr, tile_score, st, &dump);
+  if (e != hipSuccess) return hip_result(e, "score_dump select");
+  return hip_result(ugbsa::launch_score_tau(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, mode,
+                                            scaling, tau_hat, st),
+                    "score_dump tau");
+}
+
 int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode, float tau,
                  int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots, int NB,
                  float* sigma_eff, uint8_t* uncertain, float* threshold, void* stream) {

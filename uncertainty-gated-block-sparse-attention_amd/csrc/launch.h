@@ -25,11 +25,27 @@ hipError_t launch_block_summary(const uint16_t* k, int64_t sk_b, int64_t sk_h, i
                                 int B, int Hk, int N, int D, int mode, uint16_t* planes,
                                 hipStream_t stream);
 
+// Outputs of the selection kernel's dump mode (on != 0): per-tile order
+// statistics of the unforced tile scores, ranked k_slots = rho_k + 1 deep.
+struct SelectDump {
+  float* g = nullptr;        // [B, H, Qt] s(k_b - 1) - s(k_b)
+  float* r = nullptr;        // [B, H, Qt] max(s(0) - s(k_b), 1e-9)
+  float* sigma = nullptr;    // [B, H, Qt] clamp(g / r, 0, 2)
+  float* g_rho = nullptr;    // [B, H, Qt] s(rho_k - 1) - s(rho_k)
+  uint8_t* valid = nullptr;  // [Qt] visible blocks > rho_k
+  int k_b = 0, rho_k = 0, on = 0;
+};
+
 hipError_t launch_select(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                          const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
                          int mode, float scaling, int k_base, int k_slots, int want_sigma,
                          int32_t* kv_idx, float* sigma, float* tile_score,
-                         hipStream_t stream);
+                         hipStream_t stream, const SelectDump* dump = nullptr);
+
+// Per-(b, h) score-noise estimate tau_hat of the score dump.
+hipError_t launch_score_tau(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                            const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
+                            int mode, float scaling, float* tau_hat, hipStream_t stream);
 
 hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, int rmode,
                          float tau, int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots,

@@ -15,10 +15,10 @@
 //   sigma           (s[k_base-1] - s[k_base]) / max(s[0] - s[k_base], 1e-6) in
 //                   IEEE fp32 (correctly rounded division, denormals kept) (:703-707).
 //
-// Workgroup = one (b, KV head g, Q tile t) and W <= 4 of the group's query
-// heads, one wavefront per head (a group of G heads takes ceil(G / 4)
-// workgroups, so two workgroups fit a CU and one's top-k overlaps the
-// other's scoring).  The KV head's summary planes stream through LDS in
+// Workgroup = one (b, KV head g, Q tile t) and W <= 8 of the group's query
+// heads, one wavefront per head (W chosen by the launcher from the LDS the
+// row needs, so that two or more workgroups share a CU where they fit and
+// one's top-k overlaps another's scoring).  The KV head's summary planes stream through LDS in
 // chunks of CH blocks, double-buffered: chunk c + 1 is fetched into
 // registers while chunk c is scored, then stored to the other buffer, one
 // barrier per chunk.  Each wave computes its 64 x CH score chunk on MFMA
@@ -27,6 +27,10 @@
 // tile scores to its LDS row.  The row then goes through a 4-pass 8-bit radix
 // select for the k_slots-th best key, a ballot compaction of the winners
 // (ties at the cut taken in block order) and a register bitonic sort.
+//
+// Dump mode (ugbsa_score_dump, the diagnostic of src/dump_block_scores.py:
+// 137-171) runs the same scoring without the forcing, ranks k_slots =
+// rho_k + 1 scores and writes the order-statistic gaps instead of kv_idx.
 #include "common.h"
 #include "launch.h"
 
@@ -94,7 +98,8 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
     int W, int n_hc, float scaling, int k_base, int k_slots, int want_sigma,
-    int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score) {
+    int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score,
+    const SelectDump dump) {
   constexpr int KS = D / 32;
   constexpr int R = KP / 64;
   constexpr int CH = select_chunk(P, D);
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   }
   if (!active) return;   // no workgroup barrier follows
   wave_lds_sync();
-  if (lane == 0) {
+  if (lane == 0 && !dump.on) {
     trow[0] = kFMax;
     trow[n_vis - 1] = kFMax;
   }
@@ -439,23 +444,49 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     });
   });
 
-  int32_t* out = kv_idx + row_id * K;
+  if (kv_idx != nullptr) {
+    int32_t* out = kv_idx + row_id * K;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int e = lane + 64 * r;
-    if (e < K)
-      out[e] = e < n_sel ? static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(v[r])) : e;
+    for (int r = 0; r < R; ++r) {
+      const int e = lane + 64 * r;
+      if (e < K)
+        out[e] = e < n_sel ? static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(v[r])) : e;
+    }
+  }
+
+  // score of rank e (0 = best); -inf past the visible blocks
+  auto val_at = [&](int e) -> float {
+    uint64_t x = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r == (e >> 6)) x = v[r];
+    const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(x >> 32), e & 63, 64));
+    return e < n_sel ? key_float(hi) : -INFINITY;
+  };
+  if (dump.on) {
+    // src/dump_block_scores.py:161-171, on the unforced scores: g, r
+    // (clamp(min=1e-9)), sigma = clamp(g / r, 0, 2) and g_rho, NaN kept
+    // where ranks past the visible blocks meet (-inf - -inf)
+    const float s0 = val_at(0);
+    const float skm1 = val_at(dump.k_b - 1), sk = val_at(dump.k_b);
+    const float srm1 = val_at(dump.rho_k - 1), srk = val_at(dump.rho_k);
+    const float gg = skm1 - sk;
+    float rr = s0 - sk;
+    if (rr < 1e-9f) rr = 1e-9f;
+    float sg = gg / rr;
+    if (sg < 0.f) sg = 0.f;
+    if (sg > 2.f) sg = 2.f;
+    if (lane == 0) {
+      dump.g[row_id] = gg;
+      dump.r[row_id] = rr;
+      dump.sigma[row_id] = sg;
+      dump.g_rho[row_id] = srm1 - srk;
+      if (b == 0 && h == 0) dump.valid[t] = n_vis > dump.rho_k ? 1 : 0;
+    }
+    return;
   }
 
   if (want_sigma) {
-    auto val_at = [&](int e) -> float {
-      uint64_t x = 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (r == (e >> 6)) x = v[r];
-      const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(x >> 32), e & 63, 64));
-      return e < n_sel ? key_float(hi) : -INFINITY;
-    };
     const float s_top = val_at(0);
     const float a = val_at(k_base - 1);
     const float cth = val_at(k_base);
@@ -471,7 +502,7 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
                                   const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                   float scaling, int k_base, int k_slots, int want_sigma,
                                   int32_t* kv_idx, float* sigma, float* tile_score,
-                                  hipStream_t stream) {
+                                  const SelectDump& dump, hipStream_t stream) {
   const int NB = (N + kBlock - 1) / kBlock;
   const int Qt = (M + kBlock - 1) / kBlock;
   const int grp = H / Hk;
@@ -507,7 +538,7 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   if (e != hipSuccess) return e;
   kern<<<dim3(static_cast<unsigned>(wgs)), 64 * W, lds, stream>>>(
       q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, n_hc, scaling, k_base,
-      k_slots, want_sigma, kv_idx, sigma, tile_score);
+      k_slots, want_sigma, kv_idx, sigma, tile_score, dump);
   return hipGetLastError();
 }
 
@@ -516,11 +547,11 @@ static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h
                                    const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                    float scaling, int k_base, int k_slots, int want_sigma,
                                    int32_t* kv_idx, float* sigma, float* tile_score,
-                                   hipStream_t stream) {
+                                   const SelectDump& dump, hipStream_t stream) {
 #define UGBSA_SEL(KP_)                                                                    \
   return launch_select_t<D, P, KP_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,  \
                                     k_base, k_slots, want_sigma, kv_idx, sigma, tile_score, \
-                                    stream)
+                                    dump, stream)
   if (k_slots <= 64) UGBSA_SEL(64);
   if (k_slots <= 128) UGBSA_SEL(128);
   if (k_slots <= 256) UGBSA_SEL(256);
@@ -533,11 +564,13 @@ hipError_t launch_select(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t 
                          const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
                          int mode, float scaling, int k_base, int k_slots, int want_sigma,
                          int32_t* kv_idx, float* sigma, float* tile_score,
-                         hipStream_t stream) {
+                         hipStream_t stream, const SelectDump* dump) {
+  const SelectDump off{};
+  const SelectDump& dm = dump != nullptr ? *dump : off;
 #define UGBSA_SELD(D_, P_)                                                                 \
   return launch_select_kp<D_, P_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,    \
                                   k_base, k_slots, want_sigma, kv_idx, sigma, tile_score,  \
-                                  stream)
+                                  dm, stream)
   const bool quest = mode == kModeQuest;
   if (D == 64) { if (quest) UGBSA_SELD(64, 2); else UGBSA_SELD(64, 3); }
   if (D == 128) { if (quest) UGBSA_SELD(128, 2); else UGBSA_SELD(128, 3); }

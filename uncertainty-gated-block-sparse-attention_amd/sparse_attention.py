@@ -174,13 +174,9 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
     n_blocks = (N + BLOCK - 1) // BLOCK
     q_tiles = (M + block_m - 1) // block_m
     k_base, k_slots = budgets(n_blocks, sel)
-    quest = sel.mode == "quest" or (sel.mode == "router" and sel.router_score == "quest")
-    mode = _capi.MODE_QUEST if quest else _capi.MODE_MEAN
+    mode = _capi.MODE_QUEST if use_quest(sel) else _capi.MODE_MEAN
 
-    planes = torch.empty(lib.ugbsa_summary_elems(B, Hk, N, D, mode), dtype=torch.bfloat16, device=dev)
-    _capi.check(lib.ugbsa_block_summary(key_states.data_ptr(), *key_states.stride(), B, Hk, N, D,
-                                        _capi.DTYPE_BF16, mode, planes.data_ptr(), stream),
-                "block summary")
+    planes = block_summary(key_states, mode)
     is_router = sel.mode == "router" and k_base < k_slots
     kv_idx = torch.empty(B, H, q_tiles, k_slots, dtype=torch.int32, device=dev)
     sigma = torch.empty(B, H, q_tiles, dtype=torch.float32, device=dev) if is_router else None
@@ -205,6 +201,28 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
                                      res.uncertain.data_ptr(), res.threshold.data_ptr(), stream),
                     "router")
     return res
+
+
+def block_summary(key_states, mode):
+    """Kernel 1: the K-block summary planes [B, Hk, NB, P, D] bf16 of ``mode``
+    (``_capi.MODE_QUEST`` or ``_capi.MODE_MEAN``), on the current stream."""
+    B, Hk, N, D = key_states.shape
+    lib = _capi.lib()
+    key_states = _contig_rows(key_states)
+    planes = torch.empty(lib.ugbsa_summary_elems(B, Hk, N, D, mode), dtype=torch.bfloat16,
+                         device=key_states.device)
+    _capi.check(lib.ugbsa_block_summary(key_states.data_ptr(), *key_states.stride(), B, Hk, N, D,
+                                        _capi.DTYPE_BF16, mode, planes.data_ptr(),
+                                        _capi.stream_ptr(key_states.device)),
+                "block summary")
+    return planes
+
+
+def use_quest(sel: Selector = None) -> bool:
+    """Quest backbone iff mode "quest" or router with router_score "quest"
+    (src/sparse_attention.py:627-628)."""
+    sel = SEL if sel is None else sel
+    return sel.mode == "quest" or (sel.mode == "router" and sel.router_score == "quest")
 
 
 def _contig_rows(t):
