@@ -159,18 +159,53 @@ def tile_scores(q, k, scaling: float, use_quest: bool, block_m: int = 64,
     return T
 
 
-def row_scores(q, k, scaling: float, use_quest: bool, rows, block_n: int = BLOCK):
+def tile_scores_at(q, k, scaling: float, use_quest: bool, tiles, block_m: int = 64,
+                   block_n: int = BLOCK, force: bool = True):
+    """tile_score rows [B, H, len(tiles), NB] of the given Q tiles only.
+
+    The same steps as ``tile_scores`` (:623-681) restricted to a subset of
+    tiles, for spot checks at sizes where the full [B, H, Qt, NB] tensor is
+    too large for the CPU.
+    """
+    q = _f32(q)
+    B, H, M, D = q.shape
+    N = k.shape[2]
+    nb = (N + block_n - 1) // block_n
+    tiles = [int(t) for t in tiles]
+    out = np.empty((B, H, len(tiles), nb), np.float32)
+    summ = block_summaries(k, use_quest, block_n)
+    for j, t in enumerate(tiles):
+        r0 = t * block_m
+        rows = np.arange(r0, min(M, r0 + block_m))
+        s = row_scores(q, k, scaling, use_quest, rows, block_n, summ=summ)
+        if rows.size < block_m:          # zero-padded query rows score 0 (:623-625)
+            s = np.concatenate([s, np.zeros(s.shape[:2] + (block_m - rows.size, nb),
+                                            np.float32)], axis=2)
+        T = s.max(axis=2)
+        last = min(r0 + block_m - 1, N - 1)
+        T[..., np.arange(nb) * block_n > last] = -np.inf
+        if force:
+            T[..., 0] = FMAX
+            T[..., last // block_n] = FMAX
+        out[:, :, j] = T
+    return out
+
+
+def row_scores(q, k, scaling: float, use_quest: bool, rows, block_n: int = BLOCK,
+               summ=None):
     """Per-row block scores S [B, H, len(rows), NB] fp32 of the given query rows.
 
     The score of src/sparse_attention.py:638-648 (no tile max, no mask), as
     the score dump reads it for its noise estimate (src/dump_block_scores.py:
-    126-135, 181-187).
+    126-135, 181-187).  ``summ``: ``block_summaries(k, use_quest)`` if
+    already computed.
     """
     q = _f32(q)
     B, H, M, D = q.shape
     Hk = k.shape[1]
     grp = H // Hk
-    summ = block_summaries(k, use_quest, block_n)
+    if summ is None:
+        summ = block_summaries(k, use_quest, block_n)
     sc = np.float32(scaling)
     rows = np.asarray(rows, dtype=np.int64)
     nb = (summ[0] if use_quest else summ).shape[2]
@@ -301,21 +336,25 @@ def select_kv_idx_v2(q, k, scaling: float, cfg: SelectorConfig,
 
 
 def canonical_sets(kv_idx, k_base: int, n_blocks: int, block_m: int = 64,
-                   block_n: int = BLOCK):
+                   block_n: int = BLOCK, tiles=None):
     """Per (b, h, t): (base set, extra set) of visible blocks.
 
     The comparison sets of the parity contract: slots j < k_base and j >= k_base,
     keeping only real blocks the attention would visit (< NB and visible).
+    ``tiles`` gives the tile index of each entry of the Qt axis when kv_idx
+    holds a subset of tiles (default: entry t is tile t).
     Returns two lists (flattened over b, h, t) of frozensets.
     """
     kv = np.asarray(kv_idx)
     B, H, qt, _ = kv.shape
+    tix = list(range(qt)) if tiles is None else [int(t) for t in tiles]
     base, extra = [], []
     for b in range(B):
         for h in range(H):
-            for t in range(qt):
+            for j in range(qt):
+                t = tix[j]
                 lim = (t * block_m + block_m - 1) // block_n
-                row = kv[b, h, t]
+                row = kv[b, h, j]
                 ok = (row >= 0) & (row < n_blocks) & (row <= lim)
                 base.append(frozenset(row[:k_base][ok[:k_base]].tolist()))
                 extra.append(frozenset(row[k_base:][ok[k_base:]].tolist()))

@@ -37,16 +37,17 @@ def _cut_values(T_row, k):
 
 def unexplained_differences(kv_a, kv_b, T_ref, k_base, k_slots, trig_a=None, trig_b=None,
                             sig_a=None, sig_b=None, thr_a=None, thr_b=None,
-                            tol=2e-6, sig_tol=16 * OS.sigma_quantum()):
+                            tol=2e-6, sig_tol=16 * OS.sigma_quantum(), tiles=None):
     """Rows of kv_a / kv_b whose visible sets differ without a near-tie excuse.
 
     T_ref: fp32 tile scores [B, H, Qt, NB] used to judge ties (the oracle's).
     trig_*: bool [B, H, Qt] trigger decisions (router) or None.
+    tiles: tile index of each Qt entry when the arrays hold a subset of tiles.
     Returns (n_rows_differing, list of unexplained row indices).
     """
     nb = T_ref.shape[-1]
-    base_a, extra_a = OS.canonical_sets(kv_a, k_base, nb)
-    base_b, extra_b = OS.canonical_sets(kv_b, k_base, nb)
+    base_a, extra_a = OS.canonical_sets(kv_a, k_base, nb, tiles=tiles)
+    base_b, extra_b = OS.canonical_sets(kv_b, k_base, nb, tiles=tiles)
     Tf = T_ref.reshape(-1, nb)
     n_diff, bad = 0, []
     ta = None if trig_a is None else np.asarray(trig_a).reshape(-1).astype(bool)

@@ -49,9 +49,10 @@ def same_or_both_nan(a, b):
     return a.shape == b.shape and bool(np.all(both_nan | (a.view(np.uint32) == b.view(np.uint32))))
 
 
-def check_shard(shard, q, k, scaling, sel, heads=None):
+def check_shard(shard, q, k, scaling, sel, heads=None, scores=True):
     """Kernel shard vs oracle; ``heads`` limits the from-scratch oracle to a
-    slice of query heads (with their KV head) to keep big configs fast."""
+    slice of query heads (with their KV head) to keep big configs fast;
+    ``scores=False`` skips the from-scratch tile scores (long rows)."""
     T_k = shard["tile_score"].cpu().numpy()
     cfg = OS.SelectorConfig.from_selector(sel)
     nb = T_k.shape[-1]
@@ -66,10 +67,11 @@ def check_shard(shard, q, k, scaling, sel, heads=None):
     qh = q[:, hs].float().cpu().numpy()
     kh = k.float().cpu().numpy() if heads is None else \
         k[:, hs.start // (H // Hk):hs.start // (H // Hk) + 1].float().cpu().numpy()
-    T_or = OS.tile_scores(qh, kh, scaling, cfg.use_quest, force=False)
-    fin = np.isfinite(T_or)
-    assert np.array_equal(fin, np.isfinite(T_k[:, hs]))
-    assert np.abs(T_or[fin] - T_k[:, hs][fin]).max() <= 1e-5
+    if scores:
+        T_or = OS.tile_scores(qh, kh, scaling, cfg.use_quest, force=False)
+        fin = np.isfinite(T_or)
+        assert np.array_equal(fin, np.isfinite(T_k[:, hs]))
+        assert np.abs(T_or[fin] - T_k[:, hs][fin]).max() <= 1e-5
     tau_or = OD.tau_hat(qh, kh, scaling, cfg.use_quest)
     np.testing.assert_allclose(shard["tau_hat"][:, hs], tau_or, rtol=1e-4)
     return T_k
@@ -116,6 +118,19 @@ def test_score_dump_c2_full_config(hip_lib):
     assert shard["g"].shape == (1, 28, 512) and shard["tau_hat"].shape == (1, 28)
     assert shard["valid"].sum() == 512 - 128
     check_shard(shard, q, k, cfg.scaling, sel, heads=slice(0, 7))
+
+
+def test_score_dump_streaming_rows(hip_lib):
+    """Rows past 4096 blocks (the selector's streaming form) in dump mode."""
+    print("[case] score_dump streaming rows", flush=True)
+    S = 4097 * 64
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, 2, S, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 1, S, 64, generator=g).to(torch.bfloat16)
+    sel = make_sel(mode="router", router_score="quest", budget_blocks=32)
+    shard = dbs.record(q.to(DEV), k.to(DEV), 0.125, sel=sel, want_tile_score=True)
+    torch.cuda.synchronize()
+    check_shard(shard, q, k, 0.125, sel, scores=False)
 
 
 def test_score_dump_no_shard_cases(hip_lib):

@@ -220,3 +220,30 @@ def test_router_kernel_edge_cases(hip_lib):
             want_kv = kv.copy()
             want_kv[..., kb:][~want_unc] = nb
             assert np.array_equal(kvd.cpu().numpy(), want_kv)
+
+
+@pytest.mark.parametrize("case", ["random", "all_ties", "few_values"])
+def test_select_streaming_rows_exact(hip_lib, case):
+    """Rows past 4096 blocks select by streaming candidates (bounded LDS):
+    kv_idx / sigma bit-identical to the oracle on the kernel's own scores,
+    including rows where most scores tie (cut ties go to the lowest block)."""
+    print(f"[case] select streaming {case}", flush=True)
+    nb = 4097
+    S = nb * 64
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(1, 2, S, 64, generator=g)
+    k = torch.randn(1, 1, S, 64, generator=g)
+    if case == "all_ties":
+        q.zero_()                                     # every unforced score is 0
+    elif case == "few_values":
+        q = torch.randint(-1, 2, q.shape, generator=g).float() * 0.5
+        k = torch.randint(-1, 2, k.shape, generator=g).float()
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    for fields in (dict(mode="quest", budget_blocks=32),
+                   dict(mode="router", router_score="quest", budget_blocks=32,
+                        router_grain="row", router_mode="quantile", router_quantile=0.25)):
+        sel = make_sel(**fields)
+        res, o = gpu_vs_oracle_on_kernel_scores(q, k, 0.125, sel)
+        if case == "all_ties":
+            kv = res.kv_idx[0, 0, -1].cpu().numpy()
+            assert kv[0] == 0 and kv[1] == nb - 1 and list(kv[2:64]) == list(range(1, 63))

@@ -252,3 +252,22 @@ def test_router_abs_mode_triggers_all_finite():
     cfg = S.SelectorConfig(mode="router", budget_blocks=2, k_min=1, router_mode="abs")
     sel = S.select_kv_idx_v2(q, k, 0.3, cfg)
     assert np.array_equal(sel.uncertain, ~np.isnan(sel.sigma))
+
+
+def test_tile_scores_at_equals_full_tensor_rows():
+    # the subset form used by the long-context spot checks (ragged last tile)
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((1, 4, 700, 16)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 700, 16)).astype(np.float32)
+    tiles = [0, 3, 10]
+    for quest in (False, True):
+        for force in (False, True):
+            full = S.tile_scores(q, k, 0.3, quest, force=force)
+            sub = S.tile_scores_at(q, k, 0.3, quest, tiles, force=force)
+            assert np.array_equal(sub, full[:, :, tiles]), (quest, force)
+    kv = S.topk_order(full, 4)[1]                     # [1, 4, 11, 4]
+    base_sub, extra_sub = S.canonical_sets(kv[:, :, tiles], 2, 11, tiles=tiles)
+    base_all, extra_all = S.canonical_sets(kv, 2, 11)
+    pick = [h * 11 + t for h in range(4) for t in tiles]
+    assert base_sub == [base_all[i] for i in pick]
+    assert extra_sub == [extra_all[i] for i in pick]

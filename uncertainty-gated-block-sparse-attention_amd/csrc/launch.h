@@ -16,8 +16,10 @@ constexpr int kGrainRow = 1;
 constexpr int kRouterAbs = 0;
 constexpr int kRouterQuantile = 1;
 
-// Largest key-block count the selection kernel keeps in LDS per head.
-constexpr int kMaxBlocksSelect = 8192;
+// Largest key-block count the selection kernel keeps in LDS per head: a
+// wave's fp32 score row takes 4 * NB bytes, 64 KiB at 16384 blocks (1M
+// tokens), where one wave per workgroup still fits beside the chunk buffers.
+constexpr int kMaxBlocksSelect = 16384;
 // Largest k_slots the selection kernel sorts (k_max = 112 gives 448).
 constexpr int kMaxSlots = 512;
 

@@ -45,15 +45,23 @@ struct SelectLds {
   int trow_off, hist_off, cand_off;  // within a wave's region
 };
 
-__host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP, int CH) {
+// Rows longer than this many blocks select by streaming (see stream_cap).
+constexpr int kStreamBlocks = 4096;
+
+// Candidate capacity of a streaming row: composite keys kept between
+// shrinks (at least k_slots + one chunk; 4 * KP keeps shrinks rare).
+__host__ __device__ constexpr int stream_cap(int KP) { return 4 * KP > 1024 ? 4 * KP : 1024; }
+
+__host__ __device__ inline SelectLds select_lds(int P, int D, int NB, int KP, int CH,
+                                                bool stream) {
   SelectLds s;
   s.row_stride = P * D + 8;
   s.chunk_bytes = CH * s.row_stride * 2;
-  const int trow = ((NB * 4) + 15) / 16 * 16;
+  const int trow = (((stream ? CH : NB) * 4) + 15) / 16 * 16;
   s.trow_off = 0;
   s.hist_off = trow;
   s.cand_off = trow + 256 * 4;
-  s.wave_bytes = s.cand_off + KP * 8;
+  s.wave_bytes = s.cand_off + (stream ? stream_cap(KP) : KP) * 8;
   return s;
 }
 
@@ -90,10 +98,54 @@ __device__ __forceinline__ int radix_digit(const uint32_t* hist, int lane, int& 
   return __shfl(found, src, 64);
 }
 
+// Keeps the K best of the n composite keys (score key << 32 | ~block) in
+// cand, in place and in cand order: a 4-pass radix select of the K-th
+// largest score key tau, then a stable compaction of the keys above tau and
+// the first (in cand order, i.e. lowest block) of those equal to it.
+// Returns tau; n must exceed K.
+__device__ inline uint32_t shrink_cand(uint64_t* cand, int n, int K, uint32_t* hist, int lane,
+                                       uint64_t lt_mask) {
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = K;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = lane; i < 256; i += 64) hist[i] = 0;
+    wave_lds_sync();
+    for (int i = lane; i < n; i += 64) {
+      const uint32_t key = static_cast<uint32_t>(cand[i] >> 32);
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    wave_lds_sync();
+    int bin_count;
+    const int digit = radix_digit(hist, lane, remaining, bin_count);
+    prefix |= static_cast<uint32_t>(digit) << shift;
+    pmask |= 0xFFu << shift;
+    wave_lds_sync();
+  }
+  const int need_eq = remaining;
+  int out = 0, eq_seen = 0;
+  for (int base = 0; base < n; base += 64) {
+    // every lane reads its key before any lane writes, and writes land
+    // below base + 64, so the compaction can run in place
+    const int i = base + lane;
+    const uint64_t x = i < n ? cand[i] : 0ull;
+    const uint32_t key = static_cast<uint32_t>(x >> 32);
+    const bool gt = i < n && key > prefix;
+    const bool eq = i < n && key == prefix;
+    const uint64_t be = __ballot(eq);
+    const bool keep = gt || (eq && eq_seen + __popcll(be & lt_mask) < need_eq);
+    const uint64_t bk = __ballot(keep);
+    if (keep) cand[out + __popcll(bk & lt_mask)] = x;
+    out += __popcll(bk);
+    eq_seen += __popcll(be);
+  }
+  wave_lds_sync();
+  return prefix;
+}
+
 // Blocks per LDS chunk: 32 while a block's planes are at most 512 bytes, else 16.
 __host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 256 ? 32 : 16; }
 
-template <int D, int P, int KP>
+template <int D, int P, int KP, bool STREAM>
 __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
@@ -110,7 +162,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   constexpr int STAGE = (PIECES + 255) / 256;
   constexpr int QSETS = P == 2 ? 2 : 1;             // Quest: max(q, 0) and min(q, 0)
   extern __shared__ __align__(16) unsigned char smem[];
-  const SelectLds L = select_lds(P, D, NB, KP, CH);
+  const SelectLds L = select_lds(P, D, NB, KP, CH, STREAM);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -140,6 +192,14 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
 
   const int last_row = min(t * kBlock + kBlock - 1, N - 1);
   const int n_vis = last_row / kBlock + 1;           // blocks 0 .. self(t)
+  const int64_t row_id = (static_cast<int64_t>(b) * H + h) * Qt + t;
+  float* ts = tile_score != nullptr ? tile_score + row_id * NB : nullptr;
+  const int K = k_slots;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // streaming rows: candidates kept so far and the score key they all beat
+  int cnt = 0;
+  uint32_t cut = 0u;
+  bool have_cut = false;
 
   // Q tile rows as MFMA A operands (zero rows past M, as F.pad in the
   // reference); Quest keeps (max(q, 0), min(q, 0)), which multiply the
@@ -246,7 +306,33 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
           mx = -quad_rows_max(-mx);
         }
         const int blk = c * CH + 16 * nt + r16;
-        if (g4 == nt % 4 && blk < NB) trow[blk] = mx * scaling;
+        if (g4 == nt % 4 && blk < NB) trow[STREAM ? 16 * nt + r16 : blk] = mx * scaling;
+      }
+      if constexpr (STREAM) {
+        // Append the chunk's visible scores that beat the cut, in block
+        // order (forcing applied); shrink to the K best before the buffer
+        // could overflow.  The K best of the row are then always among
+        // the candidates: a later block that ties the cut ranks below every
+        // kept key of that score (higher block index).
+        wave_lds_sync();
+        const int blk = c * CH + lane;
+        const bool ok = lane < CH && blk < n_vis;
+        float sc = ok ? trow[lane] : 0.f;
+        if (!dump.on && (blk == 0 || blk == n_vis - 1)) sc = kFMax;
+        if (ok && ts != nullptr) ts[blk] = sc;
+        const uint32_t key = float_key(sc);
+        const bool take = ok && (!have_cut || key > cut);
+        const uint64_t bal = __ballot(take);
+        if (take)
+          cand[cnt + __popcll(bal & lt_mask)] =
+              (static_cast<uint64_t>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(blk));
+        cnt += __popcll(bal);
+        if (cnt > stream_cap(KP) - CH) {
+          wave_lds_sync();
+          cut = shrink_cand(cand, cnt, K, hist, lane, lt_mask);
+          cnt = K;
+          have_cut = true;
+        }
       }
     }
     if (more) store((c + 1) & 1, c + 1);
@@ -254,22 +340,22 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   }
   if (!active) return;   // no workgroup barrier follows
   wave_lds_sync();
+  const int n_sel = min(n_vis, K);
+  if constexpr (STREAM) {
+    if (ts != nullptr)
+      for (int i = n_vis + lane; i < NB; i += 64) ts[i] = -INFINITY;
+    if (cnt > K) shrink_cand(cand, cnt, K, hist, lane, lt_mask);
+  } else {
   if (lane == 0 && !dump.on) {
     trow[0] = kFMax;
     trow[n_vis - 1] = kFMax;
   }
   wave_lds_sync();
 
-  const int64_t row_id = (static_cast<int64_t>(b) * H + h) * Qt + t;
-  if (tile_score != nullptr) {
-    float* ts = tile_score + row_id * NB;
+  if (ts != nullptr)
     for (int i = lane; i < NB; i += 64) ts[i] = i < n_vis ? trow[i] : -INFINITY;
-  }
 
   // ---- top-k_slots over the n_vis visible scores ------------------------
-  const int K = k_slots;
-  const int n_sel = min(n_vis, K);
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   if (n_vis > K) {
     // Radix select of the K-th largest key tau (8-bit digits from the most
     // significant), then the keys > tau and the first (K - #greater) keys
@@ -411,6 +497,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     for (int i = lane; i < n_vis; i += 64)
       cand[i] = (static_cast<uint64_t>(float_key(trow[i])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
   }
+  }
   wave_lds_sync();
 
   uint64_t v[R];
@@ -497,7 +584,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   }
 }
 
-template <int D, int P, int KP>
+template <int D, int P, int KP, bool STREAM>
 static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                   const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                   float scaling, int k_base, int k_slots, int want_sigma,
@@ -506,7 +593,7 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   const int NB = (N + kBlock - 1) / kBlock;
   const int Qt = (M + kBlock - 1) / kBlock;
   const int grp = H / Hk;
-  const SelectLds L = select_lds(P, D, NB, KP, select_chunk(P, D));
+  const SelectLds L = select_lds(P, D, NB, KP, select_chunk(P, D), STREAM);
   constexpr int kLdsMax = 160 * 1024;
   // W heads per workgroup (ceil(grp / W) workgroups per group): the W that
   // keeps the most active wavefronts on a CU, given its LDS and at most 8
@@ -531,7 +618,7 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   if (W == 0 || 2 * L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
   const size_t lds = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(W) * L.wave_bytes;
   const int64_t wgs = static_cast<int64_t>(B) * Hk * Qt * n_hc;
-  auto kern = select_kernel<D, P, KP>;
+  auto kern = select_kernel<D, P, KP, STREAM>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds));
@@ -548,10 +635,17 @@ static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h
                                    float scaling, int k_base, int k_slots, int want_sigma,
                                    int32_t* kv_idx, float* sigma, float* tile_score,
                                    const SelectDump& dump, hipStream_t stream) {
-#define UGBSA_SEL(KP_)                                                                    \
-  return launch_select_t<D, P, KP_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,  \
-                                    k_base, k_slots, want_sigma, kv_idx, sigma, tile_score, \
-                                    dump, stream)
+  // rows of more than kStreamBlocks blocks stream their candidates, so that
+  // LDS per wave does not grow with the context
+  const bool stream_rows = (N + kBlock - 1) / kBlock > kStreamBlocks;
+#define UGBSA_SEL(KP_)                                                                      \
+  return stream_rows                                                                        \
+             ? launch_select_t<D, P, KP_, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, \
+                                                scaling, k_base, k_slots, want_sigma, kv_idx,  \
+                                                sigma, tile_score, dump, stream)               \
+             : launch_select_t<D, P, KP_, false>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,  \
+                                                 scaling, k_base, k_slots, want_sigma, kv_idx, \
+                                                 sigma, tile_score, dump, stream)
   if (k_slots <= 64) UGBSA_SEL(64);
   if (k_slots <= 128) UGBSA_SEL(128);
   if (k_slots <= 256) UGBSA_SEL(256);
