@@ -45,6 +45,9 @@ extern "C" {
 #define UGBSA_ROUTER_ABS 0  /* Selector.router_mode */
 #define UGBSA_ROUTER_QUANTILE 1
 
+#define UGBSA_V1_TOPK 0     /* per-row budget k_bud (modes topk, quest, router, rollout) */
+#define UGBSA_V1_BELIEF 1   /* per-row budget from the top_p softmax mass (mode belief) */
+
 int ugbsa_abi_version(void);
 const char* ugbsa_last_error(void);
 
@@ -109,6 +112,67 @@ int ugbsa_score_dump(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, in
 int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode, float tau,
                  int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots, int NB,
                  float* sigma_eff, uint8_t* uncertain, float* threshold, void* stream);
+
+/* ---- v1 per-row path (kernel_v2=False) ---------------------------------- */
+
+/* fp32 elements of a ugbsa_select_mask workspace that scores every row in one
+ * pass ([B, H, ceil(M / 64) * 64, NB]); any multiple of B * H * 64 * NB also
+ * works, processed in that many rows at a time. */
+int64_t ugbsa_select_mask_workspace_elems(int B, int H, int M, int N);
+
+/* Per-row block selection: keep [B, H, M, NB] uint8 (0/1, contiguous) of
+ * _block_select_mask, src/sparse_attention.py:208-295 (the router's trigger
+ * is ugbsa_router_rows).  Per query row the block scores of kernel 2's
+ * backbone (-inf past the row's visible blocks, :218-244), ranked by (score
+ * desc, block asc); kept: the k_bud best (policy UGBSA_V1_TOPK, :273-283) or
+ * the clamp(#{cumsum of sorted softmax < top_p} + 1, k_min, k_max) best
+ * (UGBSA_V1_BELIEF, :262-270, 284-285); ranks past the visible blocks keep
+ * the lowest invisible blocks; then the sink and the row's own block
+ * (:287-289).  penalty [H, NB] (or NULL) is subtracted from the scores of
+ * row M - 1 first (rollout, :247-259).  k_eff > 0 also writes margin
+ * [B, H, M] = (s[k_eff - 1] - s[k_eff]) / max(s[0] - s[k_eff], 1e-6)
+ * (:299-316).  Needs M == N, NB <= 4096; the workspace holds the row scores
+ * of the last pass on return. */
+int ugbsa_select_mask(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                      const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                      int mode, float scaling, int policy, int k_bud, int k_eff, int k_min,
+                      int k_max, float top_p, const float* penalty, float* workspace,
+                      int64_t workspace_elems, uint8_t* keep, float* margin, void* stream);
+
+/* v1 router (src/sparse_attention.py:317-354): margin_eff = margin, or its
+ * head mean for row grain; rows with more than k_eff visible blocks are
+ * eligible; quantile: thr = k_quant-th smallest of m_safe (margin_eff, +inf
+ * where ineligible or NaN) over B * M (row) or B * H * M (cell) values,
+ * uncertain = m_safe <= thr (k_quant = max(1, int(q * n_elig)) from the
+ * caller, 0 when nothing is eligible); abs: uncertain = margin_eff < tau.
+ * Uncertain cells' keep rows are set to their visible blocks.  threshold: a
+ * device float (NaN unless quantile with k_quant > 0). */
+int ugbsa_router_rows(const float* margin, int B, int H, int M, int NB, int grain, int rmode,
+                      float tau, int64_t k_quant, int k_eff, uint8_t* keep, float* margin_eff,
+                      uint8_t* uncertain, float* threshold, void* stream);
+
+/* _compute_kv_idx (src/triton_block_attn.py:125-146) of keep [B, H, M, NB]
+ * uint8 contiguous: kv_idx [B, H, Qt, NB] int32 — per block_m-row tile the
+ * blocks any row keeps, ascending, padded with NB — counts [B, H, Qt] (the
+ * caller's max is MAX_KEPT), and rowmask [B, H, Qt, NB] uint64 (or NULL):
+ * per listed block the tile rows keeping it (bit r = row t * block_m + r). */
+int ugbsa_keep_kv_idx(const uint8_t* keep, int B, int H, int M, int NB, int block_m,
+                      int32_t* kv_idx, uint64_t* rowmask, int32_t* counts, void* stream);
+
+/* Kernel 3 with per-row keep masks: replaces block_sparse_attn
+ * (src/triton_block_attn.py:149-182) and its kernel _fwd_kernel (:39-122).
+ * Arguments as ugbsa_attn_fwd, plus rowmask with kv_idx's shape and element
+ * strides (ugbsa_keep_kv_idx): a row attends to a listed block's keys only
+ * if its bit is set (and causally).  Slots are visited in order; k_slots <=
+ * 8192 for head_dim <= 128 with 64-row tiles. */
+int ugbsa_attn_fwd_rows(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                        const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                        const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                        const int32_t* kv_idx, const uint64_t* rowmask, int64_t si_b,
+                        int64_t si_h, int64_t si_t, int64_t si_s, int B, int H, int Hk, int M,
+                        int N, int D, int dtype, int Qt, int k_slots, int block_m, float scale,
+                        void* out, int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d,
+                        void* workspace, void* stream);
 
 /* Number of bf16 elements of the attention workspace: the K and V operand
  * copies of ugbsa_attn_prepare_kv (2 * B * Hk * NB * 64 * D). */

@@ -15,6 +15,9 @@ Modules
                visibility + sink/self forcing, top-k, sigma margin, router
                (row/cell grain, quantile/abs) and sentinel emission —
                ``src/sparse_attention.py:588-748`` of the reference.
+``selector_v1`` the v1 per-row selector ``_block_select_mask`` (keep mask;
+               topk / quest / router / belief / rollout) —
+               ``src/sparse_attention.py:208-382``.
 ``score_dump`` order statistics and score-noise estimate of the reference's
                score-dump diagnostic (``src/dump_block_scores.py:104-207``).
 ``attention``  block-sparse attention over ``kv_idx`` (kernel semantics of
@@ -26,4 +29,4 @@ How each function is pinned (beyond restating the reference) is listed in the
 module docstrings; the tests under ``tests/test_oracle_*.py`` hold the checks.
 """
 
-from . import selector, attention, score_dump  # noqa: F401
+from . import selector, selector_v1, attention, score_dump  # noqa: F401

@@ -25,6 +25,7 @@ DTYPE_BF16 = 0
 MODE_MEAN, MODE_QUEST = 0, 1
 GRAIN_CELL, GRAIN_ROW = 0, 1
 ROUTER_ABS, ROUTER_QUANTILE = 0, 1
+V1_TOPK, V1_BELIEF = 0, 1
 
 # Every symbol include/ugbsa.h declares, with its ctypes signature.
 _i, _i64, _f, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -38,6 +39,17 @@ SIGNATURES = {
     "ugbsa_score_dump": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _i, _i,
                               _f, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p]),
     "ugbsa_router": (_i, [_p, _i, _i, _i, _i, _i, _f, _i64, _p, _i, _i, _i, _p, _p, _p, _p]),
+    "ugbsa_select_mask_workspace_elems": (_i64, [_i, _i, _i, _i]),
+    "ugbsa_select_mask": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _i, _i,
+                               _f, _i, _i, _i, _i, _i, _f, _p, _p, _i64, _p, _p, _p]),
+    "ugbsa_router_rows": (_i, [_p, _i, _i, _i, _i, _i, _i, _f, _i64, _i, _p, _p, _p, _p, _p]),
+    "ugbsa_keep_kv_idx": (_i, [_p, _i, _i, _i, _i, _i, _p, _p, _p, _p]),
+    "ugbsa_attn_fwd_rows": (_i, [_p, _i64, _i64, _i64, _i64,
+                                 _p, _i64, _i64, _i64, _i64,
+                                 _p, _i64, _i64, _i64, _i64,
+                                 _p, _p, _i64, _i64, _i64, _i64,
+                                 _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f,
+                                 _p, _i64, _i64, _i64, _i64, _p, _p]),
     "ugbsa_attn_workspace_elems": (_i64, [_i, _i, _i, _i]),
     "ugbsa_attn_prepare_kv": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64,
                                    _i, _i, _i, _i, _i, _i, _p, _p]),

@@ -1,11 +1,13 @@
 """Block-sparse attention launchers — the MI355X counterpart of the reference's
 ``src/triton_block_attn.py`` (same function names, arguments and asserts).
 
-``block_sparse_attn_v2`` (reference ``:267-298``) launches the gfx950 HIP
-kernel ``attn_fwd_kernel`` through the C ABI; ``_compute_kv_idx`` (``:125-146``)
-and ``reference_attn`` (``:301-312``) are the torch helpers the reference's
-kernel test uses to build ``kv_idx`` from a keep mask and to form the SDPA
-reference.  Differences from the reference launcher, all additive:
+``block_sparse_attn_v2`` (reference ``:267-298``, per-tile ``kv_idx``) and
+``block_sparse_attn`` (``:149-182``, per-row ``keep`` mask) launch the gfx950
+HIP attention kernels through the C ABI; ``_compute_kv_idx`` (``:125-146``)
+runs as the HIP kernel ``keep_kv_idx_kernel`` on device tensors (and in torch
+for host tensors, as the reference's kernel test builds ``kv_idx``);
+``reference_attn`` (``:301-312``) forms the SDPA reference.  Differences from
+the reference launchers, all additive:
 
 * K/V may carry ``Hk`` heads with ``H % Hk == 0`` (GQA: query head h reads KV
   head h // (H // Hk), transformers' ``repeat_kv`` mapping), so callers need
@@ -14,6 +16,9 @@ reference.  Differences from the reference launcher, all additive:
   ``.contiguous()``); ``out`` may be any such strided view, which lets the
   dispatcher write the ``[B, S, H, D]`` layout directly.
 * ``num_warps`` / ``num_stages`` are Triton tuning knobs, accepted and ignored.
+* ``block_sparse_attn``: a query row whose keep mask selects no visible key
+  gets a zero output (the reference kernel returns the mean of the masked
+  values there); the selector never produces such rows (sink forced).
 """
 
 from __future__ import annotations
@@ -77,9 +82,74 @@ def block_sparse_attn_v2(q, k, v, kv_idx, scale, block_n=64, block_m=64,
     return out
 
 
+def keep_kv_idx(keep, block_m=64, want_rowmask=True):
+    """HIP compaction of a device keep mask [B, H, M, NB] (bool).
+
+    Returns (kv_idx [B, H, Qt, NB] int32 ascending and NB-padded, rowmask
+    [B, H, Qt, NB] int64 — bit r set where tile row r keeps the listed block —
+    or None, MAX_KEPT).  Synchronises once for MAX_KEPT, as the reference.
+    """
+    assert keep.is_cuda and keep.dtype == torch.bool and keep.dim() == 4
+    keep = keep.contiguous()
+    B, H, M, NB = keep.shape
+    qt = (M + block_m - 1) // block_m
+    kv = torch.empty(B, H, qt, NB, dtype=torch.int32, device=keep.device)
+    rm = torch.empty(B, H, qt, NB, dtype=torch.int64, device=keep.device) if want_rowmask else None
+    counts = torch.empty(B, H, qt, dtype=torch.int32, device=keep.device)
+    _capi.check(_capi.lib().ugbsa_keep_kv_idx(keep.data_ptr(), B, H, M, NB, block_m, kv.data_ptr(),
+                                              _capi.ptr(rm), counts.data_ptr(),
+                                              _capi.stream_ptr(keep.device)),
+                "keep_kv_idx")
+    max_kept = max(1, int(counts.max().item()))
+    return kv, rm, max_kept
+
+
+def block_sparse_attn(q, k, v, keep, scale, block_n=64, block_m=64,
+                      num_warps=4, num_stages=1, out=None, workspace=None):
+    """Per-row-selection block-sparse causal attention (HIP, bf16 MFMA).
+
+    q : [B, H, M, D] bf16; k, v : [B, Hk, N, D] bf16; keep : [B, H, M, NB]
+    bool (True = the row attends to the block).  Same contract as
+    src/triton_block_attn.py:149-182: per Q tile the union of its rows'
+    blocks is visited in ascending order (``_compute_kv_idx``) and each row
+    only sees the keys of its own kept blocks, causally.
+    """
+    assert q.dim() == 4 and k.shape == v.shape and q.shape[0] == k.shape[0] \
+        and q.shape[-1] == k.shape[-1], "q [B,H,M,D], k = v [B,Hk,N,D] expected"
+    assert q.is_cuda and keep.dtype == torch.bool
+    assert block_n == 64, "key blocks are 64 tokens"
+    B, H, M, D = q.shape
+    Hk, N = k.shape[1], k.shape[2]
+    assert H % Hk == 0, "query heads must be a multiple of KV heads"
+    assert tuple(keep.shape[:3]) == (B, H, M), "keep [B, H, M, NB] expected"
+    kv, rm, max_kept = keep_kv_idx(keep, block_m)
+    q = _bf16_operand("q", q)
+    k = _bf16_operand("k", k)
+    v = _bf16_operand("v", v)
+    if out is None:
+        out = torch.empty_like(q)
+    assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
+    if workspace is None:
+        workspace = attn_workspace(B, Hk, N, D, q.device)
+    rc = _capi.lib().ugbsa_attn_fwd_rows(
+        q.data_ptr(), *q.stride(),
+        k.data_ptr(), *k.stride(),
+        v.data_ptr(), *v.stride(),
+        kv.data_ptr(), rm.data_ptr(), *kv.stride(),
+        B, H, Hk, M, N, D, _capi.DTYPE_BF16, kv.shape[2], max_kept, block_m,
+        float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(),
+        _capi.stream_ptr(q.device))
+    _capi.check(rc, "block_sparse_attn")
+    return out
+
+
 def _compute_kv_idx(keep, block_m):
     """keep [B, H, M, NB] bool -> (kv_idx [B, H, Qt, MAX_KEPT] int32 ascending,
-    NB-padded; MAX_KEPT).  Same contract as src/triton_block_attn.py:125-146."""
+    NB-padded; MAX_KEPT).  Same contract as src/triton_block_attn.py:125-146:
+    the HIP kernel for device tensors, torch for host tensors."""
+    if keep.is_cuda:
+        kv, _, max_kept = keep_kv_idx(keep, block_m, want_rowmask=False)
+        return kv[..., :max_kept].contiguous(), max_kept
     B, H, M, NB = keep.shape
     q_tiles = (M + block_m - 1) // block_m
     pad = q_tiles * block_m - M

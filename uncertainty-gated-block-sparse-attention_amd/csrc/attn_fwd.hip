@@ -183,10 +183,10 @@ template <int D, int NT, int WPT, bool SPLIT, bool QLDS, bool PF>
 __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-    const uint16_t* __restrict__ vt, const int32_t* __restrict__ kv_idx, int64_t si_b,
-    int64_t si_h, int64_t si_t, int B, int Hk, int M, int N, int NB, int Qt, int k_slots,
-    float scale_signed, uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m,
-    int units, int grp) {
+    const uint16_t* __restrict__ vt, const int32_t* __restrict__ kv_idx,
+    const uint64_t* __restrict__ rowmask, int64_t si_b, int64_t si_h, int64_t si_t, int B,
+    int Hk, int M, int N, int NB, int Qt, int k_slots, float scale_signed,
+    uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m, int units, int grp) {
   using S = AttnShape<D, NT, WPT, SPLIT, QLDS, PF>;
   constexpr int BM = S::BM, KS = S::KS, DT = S::DT;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -248,7 +248,11 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; }
 
-  const int32_t* idx = kv_idx + b * si_b + h * si_h + t * si_t;
+  const int64_t idx_off = b * si_b + h * si_h + t * si_t;
+  const int32_t* idx = kv_idx + idx_off;
+  // per-row keep masks of the listed blocks (bit r: tile row r keeps it), or
+  // none: every row of the tile attends to every listed block
+  const uint64_t* rmk = rowmask != nullptr ? rowmask + idx_off : nullptr;
   // K rows of this KV head: byte offsets past N * sk_n read as zeros.
   const __amdgpu_buffer_rsrc_t krs =
       make_rsrc(k + b * sk_b + g * sk_h, static_cast<uint32_t>(static_cast<int64_t>(N) * sk_n * 2));
@@ -321,20 +325,27 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     const int s_next = next_slot(s + step);
     if (PF && s_next < k_slots) load_k(block_at(s_next), kf);
 
-    // ---- causal / bounds mask, online softmax (log2 domain) -------------
-    const bool need_mask = (kbase + kBlock - 1 > row0) || (kbase + kBlock > N);
+    // ---- causal / bounds / row-keep mask, online softmax (log2 domain) ---
+    uint64_t mk = ~0ull;
+    if (rmk != nullptr) {
+      const uint64_t x = rmk[s];
+      mk = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32))) << 32) |
+           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+    }
+    const bool need_mask = (kbase + kBlock - 1 > row0) || (kbase + kBlock > N) || mk != ~0ull;
     float mx_s[NT];
     bool grow = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int row = row0 + 16 * nt + r16;
       if (need_mask) {
+        const bool off = ((mk >> (row - t * BM)) & 1ull) == 0;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kbase + 32 * (mt >> 1) + 8 * g4 + 4 * (mt & 1) + i;
-            if (key > row || key >= N) st[mt][nt][i] = -INFINITY;
+            if (off || key > row || key >= N) st[mt][nt][i] = -INFINITY;
           }
       }
       float mx = -INFINITY;
@@ -477,10 +488,10 @@ template <int D, bool QLDS>
 __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-    const uint16_t* __restrict__ vt, const int32_t* __restrict__ kv_idx, int64_t si_b,
-    int64_t si_h, int64_t si_t, int B, int Hk, int M, int N, int NB, int Qt, int k_slots,
-    float scale_log2, uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m,
-    int units, int grp) {
+    const uint16_t* __restrict__ vt, const int32_t* __restrict__ kv_idx,
+    const uint64_t* __restrict__ rowmask, int64_t si_b, int64_t si_h, int64_t si_t, int B,
+    int Hk, int M, int N, int NB, int Qt, int k_slots, float scale_log2,
+    uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m, int units, int grp) {
   constexpr int NT = 4, KS = D / 32, DT = D / 16, BM = 64;
   extern __shared__ int32_t blist[];        // k_slots entries (dynamic LDS)
 
@@ -504,10 +515,16 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   // (the heads of a KV group and neighbouring tiles then sweep shared blocks
   // together, which keeps them in L2).  A block listed twice in a row keeps
   // the slot order, so it is visited twice as the reference loop does.
-  const int32_t* idx = kv_idx + b * si_b + h * si_h + t * si_t;
+  const int64_t idx_off = b * si_b + h * si_h + t * si_t;
+  const int32_t* idx = kv_idx + idx_off;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   uint32_t* bits = reinterpret_cast<uint32_t*>(blist + k_slots);
   const int n_words = (min(t, NB - 1) >> 5) + 1;     // visible blocks are <= t
+  // per-row keep masks of the visited blocks (bit r: tile row r keeps the
+  // block), listed beside blist; without them every row attends every block
+  const uint64_t* rmk = rowmask != nullptr ? rowmask + idx_off : nullptr;
+  uint64_t* mlist = reinterpret_cast<uint64_t*>(
+      blist + ((k_slots + (NB + 31) / 32 + 1) & ~1));
   for (int w = lane; w < n_words; w += 64) bits[w] = 0u;
   wave_lds_sync();
   int nv = 0;
@@ -519,13 +536,16 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
     const uint64_t bal = __ballot(ok);
     if (ok) {
       blist[nv + __popcll(bal & lt_mask)] = blk;
+      if (rmk != nullptr) mlist[nv + __popcll(bal & lt_mask)] = rmk[s];
       const uint32_t bit = 1u << (blk & 31);
       dup |= (atomicOr(&bits[blk >> 5], bit) & bit) != 0u;
     }
     nv += __popcll(bal);
   }
   wave_lds_sync();
-  if (__ballot(dup) == 0) {
+  // with row masks the slots are visited in their order (the masks are
+  // listed per slot); otherwise a list without repeats is re-sorted
+  if (rmk == nullptr && __ballot(dup) == 0) {
     int pos = 0;
     for (int w0 = 0; w0 < n_words; w0 += 64) {
       const int w = w0 + lane;
@@ -607,19 +627,28 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
   for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; }
   bf16x8 pb[NT];
 
-  // Causal / bounds mask (only half blocks crossing the diagonal or N).
-  auto mask = [&](SBuf& st, int blk, int half) {
+  // Row-keep mask of half block u (wave-uniform), all rows without masks.
+  auto mbits = [&](int u) -> uint64_t {
+    if (rmk == nullptr) return ~0ull;
+    const uint64_t x = mlist[clamp_u(u) >> 1];
+    return (static_cast<uint64_t>(uni(static_cast<int>(x >> 32))) << 32) |
+           static_cast<uint32_t>(uni(static_cast<int>(x)));
+  };
+  // Causal / bounds / row-keep mask (only half blocks crossing the diagonal
+  // or N, or not kept by every row).
+  auto mask = [&](SBuf& st, int blk, int half, uint64_t mk) {
     const int kbase = blk * kBlock + 32 * half;
-    if ((kbase + 31 > row0) || (kbase + 32 > N)) {
+    if ((kbase + 31 > row0) || (kbase + 32 > N) || mk != ~0ull) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int row = row0 + 16 * nt + r16;
+        const bool off = ((mk >> (16 * nt + r16)) & 1ull) == 0;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kbase + 8 * g4 + 4 * mt + i;
-            if (key > row || key >= N) st[mt][nt][i] = -INFINITY;
+            if (off || key > row || key >= N) st[mt][nt][i] = -INFINITY;
           }
       }
     }
@@ -769,7 +798,7 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
       asm volatile("" : "+v"(pin), "+v"(l[nt]));
       pb[nt] = __builtin_bit_cast(bf16x8, pin);
     }
-    mask(nxt, uni(rm1), (u + 1) & 1);
+    mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
     const bool moved = phase2(nxt, vc);
     load_v(uni(rv), clamp_u(u + 2) & 1, vc);
     if (moved) rescale();
@@ -782,7 +811,7 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
     load_v(uni(blk_raw(1)), 1, vb);
     qk(sa, ka);
     load_k(uni(blk_raw(2)), clamp_u(2) & 1, ka);
-    mask(sa, uni(blk_raw(0)), 0);
+    mask(sa, uni(blk_raw(0)), 0, mbits(0));
     if (rowmax(sa)) rescale();
     // nu = 2 * nv is even: steady steps u = 0 .. nu - 2, then the last half block.
     int u = 0;
@@ -817,27 +846,39 @@ __global__ __launch_bounds__(64) void attn_fwd_pipe_kernel(
 template <int D, bool QLDS>
 static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                    const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                                   const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
-                                   int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
-                                   int Qt, int k_slots, float scale, uint16_t* out, int64_t so_b,
+                                   const uint16_t* vt, const int32_t* kv_idx,
+                                   const uint64_t* rowmask, int64_t si_b, int64_t si_h,
+                                   int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
+                                   int k_slots, float scale, uint16_t* out, int64_t so_b,
                                    int64_t so_h, int64_t so_m, hipStream_t stream) {
   const int NB = (N + kBlock - 1) / kBlock;
   const int grp = H / Hk;
   const int units = B * Hk * Qt;
   const int64_t wgs = 8LL * grp * ((units + 7) / 8);
-  const size_t lds = static_cast<size_t>(k_slots) * 4 + static_cast<size_t>((NB + 31) / 32) * 4;
-  attn_fwd_pipe_kernel<D, QLDS><<<dim3(static_cast<unsigned>(wgs)), 64, lds, stream>>>(
-      q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b, si_h, si_t, B, Hk, M, N, NB,
-      Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
+  // block list, bitmap words, and (with row masks) one mask per listed slot
+  size_t lds = static_cast<size_t>(k_slots) * 4 + static_cast<size_t>((NB + 31) / 32) * 4;
+  if (rowmask != nullptr)
+    lds = static_cast<size_t>((k_slots + (NB + 31) / 32 + 1) & ~1) * 4 + static_cast<size_t>(k_slots) * 8;
+  auto kern = attn_fwd_pipe_kernel<D, QLDS>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  kern<<<dim3(static_cast<unsigned>(wgs)), 64, lds, stream>>>(
+      q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, Hk, M,
+      N, NB, Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
   return hipGetLastError();
 }
 
 template <int D, int NT, int WPT, bool SPLIT, bool QLDS, bool PF>
 static hipError_t launch_attn_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                 const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                                const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
-                                int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
-                                int Qt, int k_slots, float scale, uint16_t* out, int64_t so_b,
+                                const uint16_t* vt, const int32_t* kv_idx,
+                                const uint64_t* rowmask, int64_t si_b, int64_t si_h,
+                                int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
+                                int k_slots, float scale, uint16_t* out, int64_t so_b,
                                 int64_t so_h, int64_t so_m, hipStream_t stream) {
   using S = AttnShape<D, NT, WPT, SPLIT, QLDS, PF>;
   const int NB = (N + kBlock - 1) / kBlock;
@@ -849,8 +890,8 @@ static hipError_t launch_attn_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, i
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                               hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS);
   kern<<<dim3(static_cast<unsigned>(wgs)), 64 * WPT, S::LDS, stream>>>(
-      q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b, si_h, si_t, B, Hk, M, N, NB,
-      Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
+      q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, Hk, M,
+      N, NB, Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
   return hipGetLastError();
 }
 
@@ -882,19 +923,20 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
                            const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
                            int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
                            int D, int Qt, int k_slots, int block_m, float scale, uint16_t* out,
-                           int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream) {
+                           int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream,
+                           const uint64_t* rowmask) {
   int want[5] = {-1, -1, -1, -1, -1};
   if (const char* env = getenv("UGBSA_ATTN_VARIANT"))
     sscanf(env, "%d,%d,%d,%d,%d", &want[0], &want[1], &want[2], &want[3], &want[4]);
   if (uses_pipe(D, block_m)) {   // the pipelined kernel (its K/V operand layout is prepared)
     if (k_slots > kPipeMaxSlots) return hipErrorInvalidValue;
     if (D == 128)
-      return launch_attn_pipe<128, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b,
-                                          si_h, si_t, B, H, Hk, M, N, Qt, k_slots, scale, out,
-                                          so_b, so_h, so_m, stream);
-    return launch_attn_pipe<64, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b,
-                                       si_h, si_t, B, H, Hk, M, N, Qt, k_slots, scale, out, so_b,
-                                       so_h, so_m, stream);
+      return launch_attn_pipe<128, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
+                                          rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
+                                          scale, out, so_b, so_h, so_m, stream);
+    return launch_attn_pipe<64, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
+                                       rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
+                                       scale, out, so_b, so_h, so_m, stream);
   }
   bool first = true;
 #define UGBSA_TRY(D_, BM_, NT_, WPT_, SP_, QL_, PF_)                                            \
@@ -904,8 +946,8 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
     first = false;                                                                             \
     if (match)                                                                                 \
       return launch_attn_t<D_, NT_, WPT_, SP_ != 0, QL_ != 0, PF_ != 0>(                        \
-          q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b, si_h, si_t, B, H, Hk, M, \
-          N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream);                               \
+          q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, H, \
+          Hk, M, N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream);                        \
   }
   {
     UGBSA_ATTN_VARIANTS(UGBSA_TRY)

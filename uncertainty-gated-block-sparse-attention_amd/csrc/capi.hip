@@ -131,7 +131,7 @@ int ugbsa_score_dump(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, in
     return fail(UGBSA_EARG, "score dump needs 1 <= k_b < rho_k < min(NB=%d, %d) (k_b=%d, rho_k=%d)",
                 nb, ugbsa::kMaxSlots, k_b, rho_k);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  ugbsa::SelectDump dump;
+  ugbsa::SelectAux dump;
   dump.g = g;
   dump.r = r;
   dump.sigma = sigma;
@@ -139,7 +139,7 @@ int ugbsa_score_dump(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, in
   dump.valid = valid;
   dump.k_b = k_b;
   dump.rho_k = rho_k;
-  dump.on = 1;
+  dump.dump = 1;
   const uint16_t* q16 = static_cast<const uint16_t*>(q);
   const uint16_t* p16 = static_cast<const uint16_t*>(planes);
   hipError_t e = ugbsa::launch_select(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, mode, scaling,
@@ -190,13 +190,18 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
                     "attn_prepare_kv");
 }
 
-int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
-                   const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
-                   const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
-                   const int32_t* kv_idx, int64_t si_b, int64_t si_h, int64_t si_t,
-                   int64_t si_s, int B, int H, int Hk, int M, int N, int D, int dtype, int Qt,
-                   int k_slots, int block_m, float scale, void* out, int64_t so_b,
-                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                    const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                    const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                    const int32_t* kv_idx, const uint64_t* rowmask, int64_t si_b, int64_t si_h,
+                    int64_t si_t, int64_t si_s, int B, int H, int Hk, int M, int N, int D,
+                    int dtype, int Qt, int k_slots, int block_m, float scale, void* out,
+                    int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d, void* workspace,
+                    void* stream) {
   int rc = check_dims(B, H, Hk, D, dtype);
   if (rc) return rc;
   if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
@@ -218,6 +223,8 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
     return fail(UGBSA_EARG, "one KV head's K rows exceed the 4 GiB buffer-load range");
   if (k_slots > 16384 && block_m == 64 && D <= 128)
     return fail(UGBSA_EARG, "k_slots=%d exceeds the 16384-slot kv list of the attention kernel", k_slots);
+  if (rowmask != nullptr && k_slots > 8192 && block_m == 64 && D <= 128)
+    return fail(UGBSA_EARG, "k_slots=%d exceeds the 8192-slot kv list of the row-masked attention kernel", k_slots);
   if (v != nullptr) {   // NULL: the workspace already holds ugbsa_attn_prepare_kv's output
     hipError_t e = ugbsa::launch_attn_prepare(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n,
                                               static_cast<const uint16_t*>(v), sv_b, sv_h, sv_n,
@@ -228,8 +235,140 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
                                            static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, vt,
                                            kv_idx, si_b, si_h, si_t, B, H, Hk, M, N, D, Qt,
                                            k_slots, block_m, scale, static_cast<uint16_t*>(out),
-                                           so_b, so_h, so_m, st),
+                                           so_b, so_h, so_m, st, rowmask),
                     "attn_fwd");
+}
+
+}  // namespace
+
+extern "C" {
+
+int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                   const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                   const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                   const int32_t* kv_idx, int64_t si_b, int64_t si_h, int64_t si_t,
+                   int64_t si_s, int B, int H, int Hk, int M, int N, int D, int dtype, int Qt,
+                   int k_slots, int block_m, float scale, void* out, int64_t so_b,
+                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace, void* stream) {
+  return attn_fwd_common(q, sq_b, sq_h, sq_m, sq_d, k, sk_b, sk_h, sk_n, sk_d, v, sv_b, sv_h,
+                         sv_n, sv_d, kv_idx, nullptr, si_b, si_h, si_t, si_s, B, H, Hk, M, N, D,
+                         dtype, Qt, k_slots, block_m, scale, out, so_b, so_h, so_m, so_d,
+                         workspace, stream);
+}
+
+int ugbsa_attn_fwd_rows(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                        const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
+                        const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
+                        const int32_t* kv_idx, const uint64_t* rowmask, int64_t si_b,
+                        int64_t si_h, int64_t si_t, int64_t si_s, int B, int H, int Hk, int M,
+                        int N, int D, int dtype, int Qt, int k_slots, int block_m, float scale,
+                        void* out, int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d,
+                        void* workspace, void* stream) {
+  if (rowmask == nullptr) return fail(UGBSA_EARG, "rowmask is null");
+  return attn_fwd_common(q, sq_b, sq_h, sq_m, sq_d, k, sk_b, sk_h, sk_n, sk_d, v, sv_b, sv_h,
+                         sv_n, sv_d, kv_idx, rowmask, si_b, si_h, si_t, si_s, B, H, Hk, M, N, D,
+                         dtype, Qt, k_slots, block_m, scale, out, so_b, so_h, so_m, so_d,
+                         workspace, stream);
+}
+
+int ugbsa_keep_kv_idx(const uint8_t* keep, int B, int H, int M, int NB, int block_m,
+                      int32_t* kv_idx, uint64_t* rowmask, int32_t* counts, void* stream) {
+  if (keep == nullptr || kv_idx == nullptr || counts == nullptr)
+    return fail(UGBSA_EARG, "keep / kv_idx / counts is null");
+  if (B < 1 || H < 1 || M < 1 || NB < 1) return fail(UGBSA_EARG, "B, H, M, NB must be positive");
+  if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
+  return hip_result(ugbsa::launch_keep_kv_idx(keep, B, H, M, NB, block_m, kv_idx, rowmask, counts,
+                                              static_cast<hipStream_t>(stream)),
+                    "keep_kv_idx");
+}
+
+int64_t ugbsa_select_mask_workspace_elems(int B, int H, int M, int N) {
+  const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  const int64_t mp = (M + ugbsa::kBlock - 1) / ugbsa::kBlock * ugbsa::kBlock;
+  return static_cast<int64_t>(B) * H * mp * nb;
+}
+
+int ugbsa_select_mask(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                      const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                      int mode, float scaling, int policy, int k_bud, int k_eff, int k_min,
+                      int k_max, float top_p, const float* penalty, float* workspace,
+                      int64_t workspace_elems, uint8_t* keep, float* margin, void* stream) {
+  int rc = check_dims(B, H, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
+  if (M < 1 || M != N) return fail(UGBSA_EARG, "the per-row selector needs M == N >= 1 (M=%d, N=%d)", M, N);
+  if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
+  if (policy != UGBSA_V1_TOPK && policy != UGBSA_V1_BELIEF) return fail(UGBSA_EARG, "unknown v1 policy %d", policy);
+  if (planes == nullptr || !aligned16(planes)) return fail(UGBSA_ELAYOUT, "planes must be a 16-byte aligned buffer");
+  if (keep == nullptr || workspace == nullptr) return fail(UGBSA_EARG, "keep / workspace is null");
+  const int nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  if (nb > ugbsa::kStreamBlocksRows) return fail(UGBSA_EARG, "N=%d gives %d key blocks; the per-row selector holds at most %d", N, nb, ugbsa::kStreamBlocksRows);
+  if (k_eff < 0 || k_eff >= nb) return fail(UGBSA_EARG, "k_eff=%d out of range [0, NB=%d)", k_eff, nb);
+  if (k_eff > 0 && margin == nullptr) return fail(UGBSA_EARG, "margin is null (k_eff > 0)");
+  int K;
+  if (policy == UGBSA_V1_BELIEF) {
+    if (k_min < 0 || k_max < 1 || !(top_p == top_p)) return fail(UGBSA_EARG, "belief needs k_max >= 1 and a top_p");
+    K = k_max < nb ? k_max : nb;
+  } else {
+    if (k_bud < 1 || k_bud > nb) return fail(UGBSA_EARG, "k_bud=%d out of range [1, NB=%d]", k_bud, nb);
+    K = k_bud;
+  }
+  if (k_eff + 1 > K) K = k_eff + 1;
+  if (K > ugbsa::kMaxSlots) return fail(UGBSA_EARG, "ranking %d blocks deep exceeds %d", K, ugbsa::kMaxSlots);
+  const int64_t per_row = static_cast<int64_t>(B) * H * nb;
+  const int64_t chunk_tiles = workspace_elems / (per_row * ugbsa::kBlock);
+  if (chunk_tiles < 1) return fail(UGBSA_EARG, "workspace of %lld floats holds less than one 64-row tile (%lld)", (long long)workspace_elems, (long long)(per_row * ugbsa::kBlock));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Qt = (M + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  for (int t0 = 0; t0 < Qt; t0 += static_cast<int>(chunk_tiles)) {
+    const int t1 = t0 + static_cast<int>(chunk_tiles) < Qt ? t0 + static_cast<int>(chunk_tiles) : Qt;
+    ugbsa::SelectAux aux;
+    aux.row_scores = workspace;
+    aux.rows_t0 = t0;
+    aux.rows_t1 = t1;
+    hipError_t e = ugbsa::launch_select(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
+                                        static_cast<const uint16_t*>(planes), B, H, Hk, M, N, D,
+                                        mode, scaling, 1, 1, 0, nullptr, nullptr, nullptr, st, &aux);
+    if (e != hipSuccess) return hip_result(e, "select_mask row scores");
+    ugbsa::RowsArgs a;
+    a.scores = workspace;
+    a.r0 = t0 * ugbsa::kBlock;
+    a.nrows = (t1 - t0) * ugbsa::kBlock;
+    a.B = B; a.H = H; a.M = M; a.NB = nb;
+    a.K = K;
+    a.k_bud = k_bud;
+    a.belief = policy == UGBSA_V1_BELIEF;
+    a.top_p = top_p;
+    a.k_min = k_min; a.k_max = k_max;
+    a.k_eff = k_eff;
+    a.penalty = penalty;
+    a.keep = keep;
+    a.margin = k_eff > 0 ? margin : nullptr;
+    e = ugbsa::launch_select_rows(a, st);
+    if (e != hipSuccess) return hip_result(e, "select_mask rows");
+  }
+  return hip_result(hipSuccess, "select_mask");
+}
+
+int ugbsa_router_rows(const float* margin, int B, int H, int M, int NB, int grain, int rmode,
+                      float tau, int64_t k_quant, int k_eff, uint8_t* keep, float* margin_eff,
+                      uint8_t* uncertain, float* threshold, void* stream) {
+  if (margin == nullptr || keep == nullptr || margin_eff == nullptr || uncertain == nullptr ||
+      threshold == nullptr)
+    return fail(UGBSA_EARG, "margin / keep / margin_eff / uncertain / threshold is null");
+  if (B < 1 || H < 1 || M < 1 || NB < 1) return fail(UGBSA_EARG, "B, H, M, NB must be positive");
+  if (grain != UGBSA_GRAIN_CELL && grain != UGBSA_GRAIN_ROW) return fail(UGBSA_EARG, "unknown router grain %d", grain);
+  if (rmode != UGBSA_ROUTER_ABS && rmode != UGBSA_ROUTER_QUANTILE) return fail(UGBSA_EARG, "unknown router mode %d", rmode);
+  const int64_t n = (grain == UGBSA_GRAIN_ROW ? 1 : static_cast<int64_t>(H)) * B * M;
+  if (rmode == UGBSA_ROUTER_QUANTILE && (k_quant < 0 || k_quant > n))
+    return fail(UGBSA_EARG, "k_quant=%lld out of range [0, %lld]", (long long)k_quant, (long long)n);
+  if (k_eff < 1 || k_eff >= NB) return fail(UGBSA_EARG, "k_eff=%d out of range [1, NB=%d)", k_eff, NB);
+  const int64_t row0 = static_cast<int64_t>(ugbsa::kBlock) * k_eff;   // first eligible row (M == N)
+  return hip_result(ugbsa::launch_router_rows(margin, B, H, M, NB, grain, rmode, tau, k_quant,
+                                              row0 < M ? static_cast<int>(row0) : M, keep,
+                                              margin_eff, uncertain, threshold,
+                                              static_cast<hipStream_t>(stream)),
+                    "router_rows");
 }
 
 }  // extern "C"

@@ -20,6 +20,9 @@ constexpr int kRouterQuantile = 1;
 // wave's fp32 score row takes 4 * NB bytes, 64 KiB at 16384 blocks (1M
 // tokens), where one wave per workgroup still fits beside the chunk buffers.
 constexpr int kMaxBlocksSelect = 16384;
+// Largest key-block count of the per-row (v1) selector: one fp32 row of
+// scores per wavefront in LDS.
+constexpr int kStreamBlocksRows = 4096;
 // Largest k_slots the selection kernel sorts (k_max = 112 gives 448).
 constexpr int kMaxSlots = 512;
 
@@ -27,22 +30,50 @@ hipError_t launch_block_summary(const uint16_t* k, int64_t sk_b, int64_t sk_h, i
                                 int B, int Hk, int N, int D, int mode, uint16_t* planes,
                                 hipStream_t stream);
 
-// Outputs of the selection kernel's dump mode (on != 0): per-tile order
-// statistics of the unforced tile scores, ranked k_slots = rho_k + 1 deep.
-struct SelectDump {
+// Extra modes of the selection kernel.
+//  dump != 0: per-tile order statistics of the unforced tile scores, ranked
+//             k_slots = rho_k + 1 deep, written instead of kv_idx;
+//  row_scores != nullptr: the per-row scores of tiles [rows_t0, rows_t1)
+//             (rows past M skipped) into row_scores [B, H, 64 * (rows_t1 -
+//             rows_t0), NB] fp32, -inf past each tile's visible blocks, and
+//             nothing else (the v1 per-row selector's input).
+struct SelectAux {
   float* g = nullptr;        // [B, H, Qt] s(k_b - 1) - s(k_b)
   float* r = nullptr;        // [B, H, Qt] max(s(0) - s(k_b), 1e-9)
   float* sigma = nullptr;    // [B, H, Qt] clamp(g / r, 0, 2)
   float* g_rho = nullptr;    // [B, H, Qt] s(rho_k - 1) - s(rho_k)
   uint8_t* valid = nullptr;  // [Qt] visible blocks > rho_k
-  int k_b = 0, rho_k = 0, on = 0;
+  int k_b = 0, rho_k = 0, dump = 0;
+  float* row_scores = nullptr;
+  int rows_t0 = 0, rows_t1 = 0;
 };
 
 hipError_t launch_select(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                          const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
                          int mode, float scaling, int k_base, int k_slots, int want_sigma,
                          int32_t* kv_idx, float* sigma, float* tile_score,
-                         hipStream_t stream, const SelectDump* dump = nullptr);
+                         hipStream_t stream, const SelectAux* aux = nullptr);
+
+// The v1 per-row selector over a buffer of per-row scores (SelectAux
+// row_scores): one wavefront per row ranks its visible blocks K deep and
+// writes the row's keep bytes (the k_bud best, or the belief budget's best,
+// plus the sink and the row's own block) and, with k_eff > 0, its margin.
+struct RowsArgs {
+  const float* scores = nullptr;   // [B, H, nrows, NB]: rows r0 .. r0 + nrows - 1
+  int r0 = 0, nrows = 0;
+  int B = 0, H = 0, M = 0, NB = 0;
+  int K = 0;                       // ranked depth (<= 512, <= NB)
+  int k_bud = 0;                   // blocks kept per row (top-k family)
+  int belief = 0;                  // 1: budget from the top_p softmax mass
+  float top_p = 0.f;
+  int k_min = 0, k_max = 0;
+  int k_eff = 0;                   // router margin at rank k_eff (0: none)
+  const float* penalty = nullptr;  // [H, NB] subtracted from row M - 1 (rollout)
+  uint8_t* keep = nullptr;         // [B, H, M, NB]
+  float* margin = nullptr;         // [B, H, M]
+};
+
+hipError_t launch_select_rows(const RowsArgs& a, hipStream_t stream);
 
 // Per-(b, h) score-noise estimate tau_hat of the score dump.
 hipError_t launch_score_tau(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
@@ -54,6 +85,14 @@ hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, in
                          int NB, float* sigma_eff, uint8_t* uncertain, float* threshold,
                          hipStream_t stream);
 
+// v1 router: threshold over the rows' margins, trigger flags, and the keep
+// rows of uncertain cells set to their visible blocks.  threshold must be a
+// device float (the fill kernel reads it).
+hipError_t launch_router_rows(const float* margin, int B, int H, int M, int NB, int grain,
+                              int rmode, float tau, int64_t k_quant, int elig_row0,
+                              uint8_t* keep, float* margin_eff, uint8_t* uncertain,
+                              float* threshold, hipStream_t stream);
+
 hipError_t launch_attn_prepare(const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                                const uint16_t* v, int64_t sv_b, int64_t sv_h, int64_t sv_n,
                                int B, int Hk, int N, int D, int block_m, uint16_t* ws,
@@ -64,6 +103,14 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
                            const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
                            int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
                            int D, int Qt, int k_slots, int block_m, float scale, uint16_t* out,
-                           int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream);
+                           int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream,
+                           const uint64_t* rowmask = nullptr);
+
+// _compute_kv_idx on the GPU: per (b, h, block_m-row tile) the blocks any row
+// of keep [B, H, M, NB] (uint8, contiguous) keeps, ascending, NB-padded to
+// NB slots, their count, and (if rowmask) each listed block's row mask.
+hipError_t launch_keep_kv_idx(const uint8_t* keep, int B, int H, int M, int NB, int block_m,
+                              int32_t* kv_idx, uint64_t* rowmask, int32_t* counts,
+                              hipStream_t stream);
 
 }  // namespace ugbsa

@@ -20,6 +20,41 @@
 
 namespace ugbsa {
 
+// k-th smallest (1-based) of value_at(0 .. n - 1) by one workgroup: a
+// 4-pass 8-bit radix select over the order-preserving float keys (NaN above
+// every number); returns the key to every thread.
+template <class F>
+__device__ uint32_t block_kth_smallest(F value_at, int64_t n, int64_t kth, uint32_t* hist,
+                                       uint32_t* s_prefix, uint32_t* s_remaining) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (tid == 0) { *s_prefix = 0; *s_remaining = static_cast<uint32_t>(kth); }
+  uint32_t pmask = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += nt) hist[i] = 0;
+    __syncthreads();
+    const uint32_t prefix = *s_prefix;
+    for (int64_t i = tid; i < n; i += nt) {
+      const uint32_t key = float_key(value_at(i));
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {   // ascending scan for the bin holding the remaining-th smallest
+      uint32_t rem = *s_remaining, below = 0;
+      for (int d = 0; d < 256; ++d) {
+        if (below + hist[d] >= rem) {
+          *s_prefix = prefix | (static_cast<uint32_t>(d) << shift);
+          *s_remaining = rem - below;
+          break;
+        }
+        below += hist[d];
+      }
+    }
+    pmask |= 0xFFu << shift;
+    __syncthreads();
+  }
+  return *s_prefix;
+}
+
 __global__ __launch_bounds__(1024) void router_threshold_kernel(
     const float* __restrict__ sigma, int B, int H, int Qt, int grain, int rmode, float tau,
     int64_t k_quant, float* __restrict__ sigma_eff, uint8_t* __restrict__ uncertain,
@@ -56,32 +91,7 @@ __global__ __launch_bounds__(1024) void router_threshold_kernel(
       }
       return sigma_eff[i];
     };
-    if (tid == 0) { s_prefix = 0; s_remaining = static_cast<uint32_t>(kth); }
-    uint32_t pmask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid; i < 256; i += nt) hist[i] = 0;
-      __syncthreads();
-      const uint32_t prefix = s_prefix;
-      for (int64_t i = tid; i < n; i += nt) {
-        const uint32_t key = float_key(value_at(i));
-        if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (tid == 0) {   // ascending scan for the bin holding the remaining-th smallest
-        uint32_t rem = s_remaining, below = 0;
-        for (int d = 0; d < 256; ++d) {
-          if (below + hist[d] >= rem) {
-            s_prefix = prefix | (static_cast<uint32_t>(d) << shift);
-            s_remaining = rem - below;
-            break;
-          }
-          below += hist[d];
-        }
-      }
-      pmask |= 0xFFu << shift;
-      __syncthreads();
-    }
-    thr = key_float(s_prefix);
+    thr = key_float(block_kth_smallest(value_at, n, kth, hist, &s_prefix, &s_remaining));
   }
   if (tid == 0 && threshold != nullptr) *threshold = thr;
 
@@ -119,6 +129,94 @@ hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, in
     router_fill_kernel<<<dim3(static_cast<unsigned>(grid)), 256, 0, stream>>>(
         kv_idx, uncertain, rows, k_base, k_slots, NB);
   }
+  return hipGetLastError();
+}
+
+// v1 router (src/sparse_attention.py:297-354), per query row: the margins of
+// the rows (select_rows_kernel), averaged over heads in order for row grain;
+// rows with more than k_eff visible blocks (row >= elig_row0 = 64 k_eff when
+// M == N) are eligible.  Quantile: m_safe = margin, or +inf where the row is
+// not eligible or the margin is NaN; thr = k_quant-th smallest m_safe over
+// the B * M (row grain) or B * H * M (cell) entries, k_quant = max(1,
+// int(q * n_elig)) from the host (0 when nothing is eligible); uncertain =
+// m_safe <= thr and eligible.  Abs: uncertain = margin < tau and eligible.
+// An uncertain cell keeps every visible block of its row.
+__global__ __launch_bounds__(1024) void router_rows_threshold_kernel(
+    const float* __restrict__ margin, int B, int H, int M, int grain, int rmode,
+    int64_t k_quant, int elig_row0, float* __restrict__ margin_eff, float* __restrict__ threshold) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_remaining;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t n_all = static_cast<int64_t>(B) * H * M;
+  if (grain == kGrainRow) {
+    for (int64_t i = tid; i < static_cast<int64_t>(B) * M; i += nt) {
+      const int64_t b = i / M, row = i % M;
+      float acc = margin[(b * H) * M + row];
+      for (int h = 1; h < H; ++h) acc = acc + margin[(b * H + h) * M + row];
+      const float mean = acc / static_cast<float>(H);
+      for (int h = 0; h < H; ++h) margin_eff[(b * H + h) * M + row] = mean;
+    }
+  } else {
+    for (int64_t i = tid; i < n_all; i += nt) margin_eff[i] = margin[i];
+  }
+  __syncthreads();
+  if (rmode != kRouterQuantile || k_quant < 1) {
+    if (tid == 0 && threshold != nullptr) *threshold = __uint_as_float(0x7FC00000u);
+    return;
+  }
+  const int64_t n = grain == kGrainRow ? static_cast<int64_t>(B) * M : n_all;
+  auto m_safe = [&](int64_t i) -> float {
+    int64_t row, at;
+    if (grain == kGrainRow) {
+      row = i % M;
+      at = ((i / M) * H) * M + row;
+    } else {
+      row = i % M;
+      at = i;
+    }
+    const float e = margin_eff[at];
+    return (row >= elig_row0 && e == e) ? e : INFINITY;
+  };
+  const float thr = key_float(block_kth_smallest(m_safe, n, k_quant, hist, &s_prefix, &s_remaining));
+  if (tid == 0 && threshold != nullptr) *threshold = thr;
+}
+
+__global__ __launch_bounds__(256) void router_rows_fill_kernel(
+    const float* __restrict__ margin_eff, const float* __restrict__ threshold, int B, int H,
+    int M, int NB, int rmode, float tau, int64_t k_quant, int elig_row0,
+    uint8_t* __restrict__ uncertain, uint8_t* __restrict__ keep) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (i >= static_cast<int64_t>(B) * H * M) return;
+  const int row = static_cast<int>(i % M);
+  const bool elig = row >= elig_row0;
+  const float e = margin_eff[i];
+  bool unc;
+  if (rmode == kRouterQuantile) {
+    const float ms = e == e ? e : INFINITY;
+    unc = k_quant > 0 && elig && ms <= *threshold;
+  } else {
+    unc = elig && e < tau;
+  }
+  if (lane == 0) uncertain[i] = unc ? 1 : 0;
+  if (unc) {
+    uint8_t* kr = keep + i * NB;
+    const int last = row / kBlock;
+    for (int blk = lane; blk < NB; blk += 64) kr[blk] = blk <= last ? 1 : 0;
+  }
+}
+
+hipError_t launch_router_rows(const float* margin, int B, int H, int M, int NB, int grain,
+                              int rmode, float tau, int64_t k_quant, int elig_row0,
+                              uint8_t* keep, float* margin_eff, uint8_t* uncertain,
+                              float* threshold, hipStream_t stream) {
+  router_rows_threshold_kernel<<<1, 1024, 0, stream>>>(margin, B, H, M, grain, rmode, k_quant,
+                                                       elig_row0, margin_eff, threshold);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t rows = static_cast<int64_t>(B) * H * M;
+  router_rows_fill_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), 256, 0, stream>>>(
+      margin_eff, threshold, B, H, M, NB, rmode, tau, k_quant, elig_row0, uncertain, keep);
   return hipGetLastError();
 }
 

@@ -142,220 +142,11 @@ __device__ inline uint32_t shrink_cand(uint64_t* cand, int n, int K, uint32_t* h
   return prefix;
 }
 
-// Blocks per LDS chunk: 32 while a block's planes are at most 512 bytes, else 16.
-__host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 256 ? 32 : 16; }
-
-template <int D, int P, int KP, bool STREAM>
-__global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
-    const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
-    const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
-    int W, int n_hc, float scaling, int k_base, int k_slots, int want_sigma,
-    int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score,
-    const SelectDump dump) {
-  constexpr int KS = D / 32;
-  constexpr int R = KP / 64;
-  constexpr int CH = select_chunk(P, D);
-  constexpr int NT = CH / 16;                       // MFMA column tiles per chunk
-  constexpr int PIECES = CH * P * D / 8;            // 16-byte pieces per chunk
-  // pieces a thread prefetches into registers (enough for 4 or more waves;
-  // smaller workgroups copy the rest when the chunk is stored)
-  constexpr int STAGE = (PIECES + 255) / 256;
-  constexpr int QSETS = P == 2 ? 2 : 1;             // Quest: max(q, 0) and min(q, 0)
-  extern __shared__ __align__(16) unsigned char smem[];
-  const SelectLds L = select_lds(P, D, NB, KP, CH, STREAM);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int g4 = lane >> 4, r16 = lane & 15;
-  const int nthreads = blockDim.x;
-
-  const int unit = blockIdx.x / n_hc;
-  const int hc = blockIdx.x % n_hc;
-  const int per_t = B * Hk;
-  const int t = Qt - 1 - unit / per_t;
-  const int b = (unit % per_t) / Hk;
-  const int g = (unit % per_t) % Hk;
-  const int jh = hc * W + wave;
-  const bool active = jh < grp;
-  const int h = g * grp + (active ? jh : 0);
-  const int H = Hk * grp;
-
-  // chunk buffer i at smem + i * chunk_bytes (derived from smem each time, so
-  // the compiler keeps LDS addressing for the operand reads)
-  auto chunk_buf = [&](int i) -> uint16_t* {
-    return reinterpret_cast<uint16_t*>(smem + i * L.chunk_bytes);
-  };
-  unsigned char* wreg = smem + 2 * L.chunk_bytes + wave * L.wave_bytes;
-  float* trow = reinterpret_cast<float*>(wreg + L.trow_off);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(wreg + L.hist_off);
-  uint64_t* cand = reinterpret_cast<uint64_t*>(wreg + L.cand_off);
-
-  const int last_row = min(t * kBlock + kBlock - 1, N - 1);
-  const int n_vis = last_row / kBlock + 1;           // blocks 0 .. self(t)
-  const int64_t row_id = (static_cast<int64_t>(b) * H + h) * Qt + t;
-  float* ts = tile_score != nullptr ? tile_score + row_id * NB : nullptr;
-  const int K = k_slots;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  // streaming rows: candidates kept so far and the score key they all beat
-  int cnt = 0;
-  uint32_t cut = 0u;
-  bool have_cut = false;
-
-  // Q tile rows as MFMA A operands (zero rows past M, as F.pad in the
-  // reference); Quest keeps (max(q, 0), min(q, 0)), which multiply the
-  // K-max and K-min planes.
-  bf16x8 qf[QSETS][4][KS];
-  {
-    const uint16_t* qb = q + b * sq_b + h * sq_h;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int row = t * kBlock + 16 * mt + r16;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 x = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
-                                             : zero_bf16x8();
-        if constexpr (P == 2) {
-          qf[0][mt][ks] = bf16_pos(x);
-          qf[QSETS - 1][mt][ks] = bf16_neg(x);
-        } else {
-          qf[0][mt][ks] = x;
-        }
-      }
-    }
-  }
-
-  const uint16_t* pl = planes + (static_cast<int64_t>(b) * Hk + g) * NB * P * D;
-  constexpr int pieces_per_blk = P * D / 8;
-  const int n_chunks = (n_vis + CH - 1) / CH;
-  u32x4 stage[STAGE];
-  auto fetch = [&](int c) {
-#pragma unroll
-    for (int j = 0; j < STAGE; ++j) {
-      const int pi = threadIdx.x + j * nthreads;
-      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
-      const int blk = c * CH + bl;
-      stage[j] = u32x4{0u, 0u, 0u, 0u};
-      if (pi < PIECES && blk < NB)
-        stage[j] = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
-    }
-  };
-  auto store = [&](int buf, int c) {
-#pragma unroll
-    for (int j = 0; j < STAGE; ++j) {
-      const int pi = threadIdx.x + j * nthreads;
-      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
-      if (pi < PIECES) *reinterpret_cast<u32x4*>(chunk_buf(buf) + bl * L.row_stride + off * 8) = stage[j];
-    }
-    for (int pi = threadIdx.x + STAGE * nthreads; pi < PIECES; pi += nthreads) {
-      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
-      const int blk = c * CH + bl;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (blk < NB) v = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
-      *reinterpret_cast<u32x4*>(chunk_buf(buf) + bl * L.row_stride + off * 8) = v;
-    }
-  };
-  const bool pos_scale = scaling >= 0.f;
-
-  fetch(0);
-  store(0, 0);
-  __syncthreads();
-  for (int c = 0; c < n_chunks; ++c) {
-    const bool more = c + 1 < n_chunks;
-    if (more) fetch(c + 1);
-    if (active) {
-      const uint16_t* chunk = chunk_buf(c & 1);
-      f32x4 acc[4][NT];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          bf16x8 bfr[NT];
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt)
-            bfr[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
-                                                       p * D + 32 * ks + 8 * g4);
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const bf16x8 a = qf[P == 2 ? p : 0][mt][ks];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma16x16x32(a, bfr[nt], acc[mt][nt]);
-          }
-        }
-      }
-      // tile max over the 64 rows of (score * scaling): the max (min for a
-      // negative scaling) of the raw sums, scaled once — fl(x * s) is
-      // monotone in x, so this is the max of the scaled scores exactly.
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        float mx = acc[0][nt][0];
-        if (pos_scale) {
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i]);
-          mx = quad_rows_max(mx);
-        } else {
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fminf(mx, acc[mt][nt][i]);
-          mx = -quad_rows_max(-mx);
-        }
-        const int blk = c * CH + 16 * nt + r16;
-        if (g4 == nt % 4 && blk < NB) trow[STREAM ? 16 * nt + r16 : blk] = mx * scaling;
-      }
-      if constexpr (STREAM) {
-        // Append the chunk's visible scores that beat the cut, in block
-        // order (forcing applied); shrink to the K best before the buffer
-        // could overflow.  The K best of the row are then always among
-        // the candidates: a later block that ties the cut ranks below every
-        // kept key of that score (higher block index).
-        wave_lds_sync();
-        const int blk = c * CH + lane;
-        const bool ok = lane < CH && blk < n_vis;
-        float sc = ok ? trow[lane] : 0.f;
-        if (!dump.on && (blk == 0 || blk == n_vis - 1)) sc = kFMax;
-        if (ok && ts != nullptr) ts[blk] = sc;
-        const uint32_t key = float_key(sc);
-        const bool take = ok && (!have_cut || key > cut);
-        const uint64_t bal = __ballot(take);
-        if (take)
-          cand[cnt + __popcll(bal & lt_mask)] =
-              (static_cast<uint64_t>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(blk));
-        cnt += __popcll(bal);
-        if (cnt > stream_cap(KP) - CH) {
-          wave_lds_sync();
-          cut = shrink_cand(cand, cnt, K, hist, lane, lt_mask);
-          cnt = K;
-          have_cut = true;
-        }
-      }
-    }
-    if (more) store((c + 1) & 1, c + 1);
-    __syncthreads();
-  }
-  if (!active) return;   // no workgroup barrier follows
-  wave_lds_sync();
-  const int n_sel = min(n_vis, K);
-  if constexpr (STREAM) {
-    if (ts != nullptr)
-      for (int i = n_vis + lane; i < NB; i += 64) ts[i] = -INFINITY;
-    if (cnt > K) shrink_cand(cand, cnt, K, hist, lane, lt_mask);
-  } else {
-  if (lane == 0 && !dump.on) {
-    trow[0] = kFMax;
-    trow[n_vis - 1] = kFMax;
-  }
-  wave_lds_sync();
-
-  if (ts != nullptr)
-    for (int i = lane; i < NB; i += 64) ts[i] = i < n_vis ? trow[i] : -INFINITY;
-
-  // ---- top-k_slots over the n_vis visible scores ------------------------
+// Top-K of trow[0 .. n_vis) by (score desc, block asc) into cand[0 ..
+// min(n_vis, K)) as composite keys (score key << 32 | ~block), unordered.
+// The wave's LDS row, histogram and candidate buffer; wave-local.
+__device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int K, uint32_t* hist,
+                                               uint64_t* cand, int lane, uint64_t lt_mask) {
   if (n_vis > K) {
     // Radix select of the K-th largest key tau (8-bit digits from the most
     // significant), then the keys > tau and the first (K - #greater) keys
@@ -497,10 +288,14 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     for (int i = lane; i < n_vis; i += 64)
       cand[i] = (static_cast<uint64_t>(float_key(trow[i])) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
   }
-  }
-  wave_lds_sync();
+}
 
-  uint64_t v[R];
+// Loads cand[0 .. n_sel) into v (element e = lane + 64 r) and sorts it
+// descending: a register bitonic sort over KP elements.
+template <int KP>
+__device__ __forceinline__ void sort_cand(const uint64_t* cand, int n_sel, int lane,
+                                          uint64_t (&v)[KP / 64]) {
+  constexpr int R = KP / 64;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int e = lane + 64 * r;
@@ -530,6 +325,265 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       for (int r = 0; r < R; ++r) v[r] = nv[r];
     });
   });
+}
+
+// Score of rank e (0 = best) of a sorted v; -inf at ranks past n_sel.
+template <int R>
+__device__ __forceinline__ float sorted_value(const uint64_t (&v)[R], int e, int n_sel) {
+  uint64_t x = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r == (e >> 6)) x = v[r];
+  const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(x >> 32), e & 63, 64));
+  return e < n_sel ? key_float(hi) : -INFINITY;
+}
+
+// Blocks per LDS chunk: 32 while a block's planes are at most 512 bytes, else 16.
+__host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 256 ? 32 : 16; }
+
+template <int D, int P, int KP, bool STREAM, bool ROWS>
+__global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
+    const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+    const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
+    int W, int n_hc, float scaling, int k_base, int k_slots, int want_sigma,
+    int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score,
+    const SelectAux aux) {
+  constexpr int KS = D / 32;
+  constexpr int R = KP / 64;
+  constexpr int CH = select_chunk(P, D);
+  constexpr int NT = CH / 16;                       // MFMA column tiles per chunk
+  constexpr int PIECES = CH * P * D / 8;            // 16-byte pieces per chunk
+  // pieces a thread prefetches into registers (enough for 4 or more waves;
+  // smaller workgroups copy the rest when the chunk is stored)
+  constexpr int STAGE = (PIECES + 255) / 256;
+  constexpr int QSETS = P == 2 ? 2 : 1;             // Quest: max(q, 0) and min(q, 0)
+  extern __shared__ __align__(16) unsigned char smem[];
+  const SelectLds L = select_lds(P, D, NB, KP, CH, STREAM);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int nthreads = blockDim.x;
+
+  const int unit = blockIdx.x / n_hc;
+  const int hc = blockIdx.x % n_hc;
+  const int per_t = B * Hk;
+  const int t = (ROWS ? aux.rows_t1 : Qt) - 1 - unit / per_t;
+  const int b = (unit % per_t) / Hk;
+  const int g = (unit % per_t) % Hk;
+  const int jh = hc * W + wave;
+  const bool active = jh < grp;
+  const int h = g * grp + (active ? jh : 0);
+  const int H = Hk * grp;
+
+  // chunk buffer i at smem + i * chunk_bytes (derived from smem each time, so
+  // the compiler keeps LDS addressing for the operand reads)
+  auto chunk_buf = [&](int i) -> uint16_t* {
+    return reinterpret_cast<uint16_t*>(smem + i * L.chunk_bytes);
+  };
+  unsigned char* wreg = smem + 2 * L.chunk_bytes + wave * L.wave_bytes;
+  float* trow = reinterpret_cast<float*>(wreg + L.trow_off);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(wreg + L.hist_off);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(wreg + L.cand_off);
+
+  const int last_row = min(t * kBlock + kBlock - 1, N - 1);
+  const int n_vis = last_row / kBlock + 1;           // blocks 0 .. self(t)
+  const int64_t row_id = (static_cast<int64_t>(b) * H + h) * Qt + t;
+  float* ts = tile_score != nullptr ? tile_score + row_id * NB : nullptr;
+  const int K = k_slots;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // streaming rows: candidates kept so far and the score key they all beat
+  int cnt = 0;
+  uint32_t cut = 0u;
+  bool have_cut = false;
+
+  // Q tile rows as MFMA A operands (zero rows past M, as F.pad in the
+  // reference); Quest keeps (max(q, 0), min(q, 0)), which multiply the
+  // K-max and K-min planes.
+  bf16x8 qf[QSETS][4][KS];
+  {
+    const uint16_t* qb = q + b * sq_b + h * sq_h;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int row = t * kBlock + 16 * mt + r16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 x = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
+                                             : zero_bf16x8();
+        if constexpr (P == 2) {
+          qf[0][mt][ks] = bf16_pos(x);
+          qf[QSETS - 1][mt][ks] = bf16_neg(x);
+        } else {
+          qf[0][mt][ks] = x;
+        }
+      }
+    }
+  }
+
+  const uint16_t* pl = planes + (static_cast<int64_t>(b) * Hk + g) * NB * P * D;
+  constexpr int pieces_per_blk = P * D / 8;
+  const int n_chunks = (n_vis + CH - 1) / CH;
+  u32x4 stage[STAGE];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < STAGE; ++j) {
+      const int pi = threadIdx.x + j * nthreads;
+      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
+      const int blk = c * CH + bl;
+      stage[j] = u32x4{0u, 0u, 0u, 0u};
+      if (pi < PIECES && blk < NB)
+        stage[j] = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
+    }
+  };
+  auto store = [&](int buf, int c) {
+#pragma unroll
+    for (int j = 0; j < STAGE; ++j) {
+      const int pi = threadIdx.x + j * nthreads;
+      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
+      if (pi < PIECES) *reinterpret_cast<u32x4*>(chunk_buf(buf) + bl * L.row_stride + off * 8) = stage[j];
+    }
+    for (int pi = threadIdx.x + STAGE * nthreads; pi < PIECES; pi += nthreads) {
+      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
+      const int blk = c * CH + bl;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (blk < NB) v = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
+      *reinterpret_cast<u32x4*>(chunk_buf(buf) + bl * L.row_stride + off * 8) = v;
+    }
+  };
+  const bool pos_scale = scaling >= 0.f;
+
+  fetch(0);
+  store(0, 0);
+  __syncthreads();
+  for (int c = 0; c < n_chunks; ++c) {
+    const bool more = c + 1 < n_chunks;
+    if (more) fetch(c + 1);
+    if (active) {
+      const uint16_t* chunk = chunk_buf(c & 1);
+      f32x4 acc[4][NT];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          bf16x8 bfr[NT];
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            bfr[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
+                                                       p * D + 32 * ks + 8 * g4);
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            const bf16x8 a = qf[P == 2 ? p : 0][mt][ks];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma16x16x32(a, bfr[nt], acc[mt][nt]);
+          }
+        }
+      }
+      if constexpr (ROWS) {
+        // per-row scores (the v1 selector's input): fl(raw * scaling), -inf
+        // past the tile's visible blocks, rows past M skipped
+        const int64_t nrows = 64 * static_cast<int64_t>(aux.rows_t1 - aux.rows_t0);
+        float* rs = aux.row_scores + (static_cast<int64_t>(b) * H + h) * nrows * NB +
+                    static_cast<int64_t>(t - aux.rows_t0) * 64 * NB;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = 16 * mt + 4 * g4 + i;
+              const int blk = c * CH + 16 * nt + r16;
+              if (t * kBlock + r < M && blk < NB)
+                rs[static_cast<int64_t>(r) * NB + blk] = blk < n_vis ? acc[mt][nt][i] * scaling : -INFINITY;
+            }
+      } else {
+        // tile max over the 64 rows of (score * scaling): the max (min for a
+        // negative scaling) of the raw sums, scaled once — fl(x * s) is
+        // monotone in x, so this is the max of the scaled scores exactly.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float mx = acc[0][nt][0];
+          if (pos_scale) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i]);
+            mx = quad_rows_max(mx);
+          } else {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) mx = fminf(mx, acc[mt][nt][i]);
+            mx = -quad_rows_max(-mx);
+          }
+          const int blk = c * CH + 16 * nt + r16;
+          if (g4 == nt % 4 && blk < NB) trow[STREAM ? 16 * nt + r16 : blk] = mx * scaling;
+        }
+        if constexpr (STREAM) {
+          // Append the chunk's visible scores that beat the cut, in block
+          // order (forcing applied); shrink to the K best before the buffer
+          // could overflow.  The K best of the row are then always among
+          // the candidates: a later block that ties the cut ranks below every
+          // kept key of that score (higher block index).
+          wave_lds_sync();
+          const int blk = c * CH + lane;
+          const bool ok = lane < CH && blk < n_vis;
+          float sc = ok ? trow[lane] : 0.f;
+          if (!aux.dump && (blk == 0 || blk == n_vis - 1)) sc = kFMax;
+          if (ok && ts != nullptr) ts[blk] = sc;
+          const uint32_t key = float_key(sc);
+          const bool take = ok && (!have_cut || key > cut);
+          const uint64_t bal = __ballot(take);
+          if (take)
+            cand[cnt + __popcll(bal & lt_mask)] =
+                (static_cast<uint64_t>(key) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(blk));
+          cnt += __popcll(bal);
+          if (cnt > stream_cap(KP) - CH) {
+            wave_lds_sync();
+            cut = shrink_cand(cand, cnt, K, hist, lane, lt_mask);
+            cnt = K;
+            have_cut = true;
+          }
+        }
+      }
+    }
+    if (more) store((c + 1) & 1, c + 1);
+    __syncthreads();
+  }
+  if (!active) return;   // no workgroup barrier follows
+  if constexpr (ROWS) {
+    // blocks past the last computed chunk: -inf
+    const int64_t nrows = 64 * static_cast<int64_t>(aux.rows_t1 - aux.rows_t0);
+    float* rs = aux.row_scores + (static_cast<int64_t>(b) * H + h) * nrows * NB +
+                static_cast<int64_t>(t - aux.rows_t0) * 64 * NB;
+    const int r_end = min(kBlock, M - t * kBlock);
+    for (int r = 0; r < r_end; ++r)
+      for (int blk = n_chunks * CH + lane; blk < NB; blk += 64) rs[static_cast<int64_t>(r) * NB + blk] = -INFINITY;
+    return;
+  }
+  wave_lds_sync();
+  const int n_sel = min(n_vis, K);
+  if constexpr (STREAM) {
+    if (ts != nullptr)
+      for (int i = n_vis + lane; i < NB; i += 64) ts[i] = -INFINITY;
+    if (cnt > K) shrink_cand(cand, cnt, K, hist, lane, lt_mask);
+  } else {
+    if (lane == 0 && !aux.dump) {
+      trow[0] = kFMax;
+      trow[n_vis - 1] = kFMax;
+    }
+    wave_lds_sync();
+    if (ts != nullptr)
+      for (int i = lane; i < NB; i += 64) ts[i] = i < n_vis ? trow[i] : -INFINITY;
+    select_to_cand(trow, n_vis, K, hist, cand, lane, lt_mask);
+  }
+  wave_lds_sync();
+
+  uint64_t v[R];
+  sort_cand<KP>(cand, n_sel, lane, v);
 
   if (kv_idx != nullptr) {
     int32_t* out = kv_idx + row_id * K;
@@ -541,22 +595,14 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     }
   }
 
-  // score of rank e (0 = best); -inf past the visible blocks
-  auto val_at = [&](int e) -> float {
-    uint64_t x = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (r == (e >> 6)) x = v[r];
-    const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(x >> 32), e & 63, 64));
-    return e < n_sel ? key_float(hi) : -INFINITY;
-  };
-  if (dump.on) {
+  auto val_at = [&](int e) -> float { return sorted_value<R>(v, e, n_sel); };
+  if (aux.dump) {
     // src/dump_block_scores.py:161-171, on the unforced scores: g, r
     // (clamp(min=1e-9)), sigma = clamp(g / r, 0, 2) and g_rho, NaN kept
     // where ranks past the visible blocks meet (-inf - -inf)
     const float s0 = val_at(0);
-    const float skm1 = val_at(dump.k_b - 1), sk = val_at(dump.k_b);
-    const float srm1 = val_at(dump.rho_k - 1), srk = val_at(dump.rho_k);
+    const float skm1 = val_at(aux.k_b - 1), sk = val_at(aux.k_b);
+    const float srm1 = val_at(aux.rho_k - 1), srk = val_at(aux.rho_k);
     const float gg = skm1 - sk;
     float rr = s0 - sk;
     if (rr < 1e-9f) rr = 1e-9f;
@@ -564,11 +610,11 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     if (sg < 0.f) sg = 0.f;
     if (sg > 2.f) sg = 2.f;
     if (lane == 0) {
-      dump.g[row_id] = gg;
-      dump.r[row_id] = rr;
-      dump.sigma[row_id] = sg;
-      dump.g_rho[row_id] = srm1 - srk;
-      if (b == 0 && h == 0) dump.valid[t] = n_vis > dump.rho_k ? 1 : 0;
+      aux.g[row_id] = gg;
+      aux.r[row_id] = rr;
+      aux.sigma[row_id] = sg;
+      aux.g_rho[row_id] = srm1 - srk;
+      if (b == 0 && h == 0) aux.valid[t] = n_vis > aux.rho_k ? 1 : 0;
     }
     return;
   }
@@ -584,12 +630,139 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   }
 }
 
-template <int D, int P, int KP, bool STREAM>
+// v1 per-row selection (src/sparse_attention.py:245-295, 299-325 for the
+// margin): one wavefront per query row.  The row's visible scores (blocks
+// 0 .. row / 64, M == N) are ranked K deep by the same radix select and
+// bitonic sort as the tile selector; the kept blocks are the count best —
+// count = k_bud, or for belief clamp(#{j : cumsum_j < top_p} + 1, k_min,
+// k_max) over the sorted softmax probabilities — then ranks past the
+// visible blocks take the lowest invisible blocks (the total order's -inf
+// ties), and the sink and the row's own block are forced.  The keep row is
+// assembled as flags in the wave's LDS row and written once.
+__host__ __device__ constexpr int rows_wave_bytes(int NB, int KP) {
+  return (NB * 4 + 15) / 16 * 16 + 256 * 4 + KP * 8;
+}
+
+template <int KP>
+__global__ __launch_bounds__(256) void select_rows_kernel(const RowsArgs a) {
+  constexpr int R = KP / 64;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (gid >= static_cast<int64_t>(a.B) * a.H * a.nrows) return;
+  const int64_t bh = gid / a.nrows;
+  const int row = a.r0 + static_cast<int>(gid % a.nrows);
+  if (row >= a.M) return;
+  const int h = static_cast<int>(bh % a.H);
+  const int NB = a.NB;
+  unsigned char* wreg = smem + wave * rows_wave_bytes(NB, KP);
+  float* trow = reinterpret_cast<float*>(wreg);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(wreg + (NB * 4 + 15) / 16 * 16);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(wreg + (NB * 4 + 15) / 16 * 16 + 1024);
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+
+  const int n_vis = row / kBlock + 1;
+  const float* src = a.scores + gid * NB;
+  const bool pen = a.penalty != nullptr && row == a.M - 1;
+  for (int blk = lane; blk < n_vis; blk += 64)
+    trow[blk] = pen ? src[blk] - a.penalty[static_cast<int64_t>(h) * NB + blk] : src[blk];
+  wave_lds_sync();
+
+  const int K = a.K;
+  select_to_cand(trow, n_vis, K, hist, cand, lane, lt_mask);
+  wave_lds_sync();
+  const int n_sel = min(n_vis, K);
+  uint64_t v[R];
+  sort_cand<KP>(cand, n_sel, lane, v);
+
+  int count = a.k_bud;
+  if (a.belief) {
+    // softmax over the visible blocks (max-subtracted, fp32), then the
+    // cumulative mass of the sorted probabilities
+    const float mx = sorted_value<R>(v, 0, n_sel);
+    float z = 0.f;
+    for (int blk = lane; blk < n_vis; blk += 64) z += expf(trow[blk] - mx);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) z += shfl_xor_f(z, m);
+    float carry = 0.f;
+    int cnt = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int e = lane + 64 * r;
+      float c = e < n_sel ? expf(key_float(static_cast<uint32_t>(v[r] >> 32)) - mx) / z : 0.f;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(c, d, 64);
+        if (lane >= d) c += o;
+      }
+      c += carry;
+      carry = __shfl(c, 63, 64);
+      cnt += __popcll(__ballot(e < K && c < a.top_p));
+    }
+    count = cnt + 1;
+    if (count < a.k_min) count = a.k_min;
+    if (count > a.k_max) count = a.k_max;
+  }
+
+  // keep flags in the LDS row (its scores are no longer needed)
+  uint32_t* flag = reinterpret_cast<uint32_t*>(trow);
+  wave_lds_sync();
+  for (int blk = lane; blk < NB; blk += 64) flag[blk] = 0u;
+  wave_lds_sync();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int e = lane + 64 * r;
+    if (e < n_sel && e < count) flag[0xFFFFFFFFu - static_cast<uint32_t>(v[r])] = 1u;
+  }
+  for (int blk = n_vis + lane; blk < min(count, NB); blk += 64) flag[blk] = 1u;
+  if (lane == 0) {
+    flag[0] = 1u;
+    flag[row / kBlock] = 1u;
+  }
+  wave_lds_sync();
+  uint8_t* kr = a.keep + (bh * a.M + row) * NB;
+  for (int blk = lane; blk < NB; blk += 64) kr[blk] = static_cast<uint8_t>(flag[blk]);
+
+  if (a.margin != nullptr) {
+    // (s[k_eff - 1] - s[k_eff]) / max(s[0] - s[k_eff], 1e-6); NaN kept
+    const float s_top = sorted_value<R>(v, 0, n_sel);
+    const float s_km1 = sorted_value<R>(v, a.k_eff - 1, n_sel);
+    const float s_k = sorted_value<R>(v, a.k_eff, n_sel);
+    float spread = s_top - s_k;
+    if (spread < 1e-6f) spread = 1e-6f;
+    const float mg = (s_km1 - s_k) / spread;
+    if (lane == 0) a.margin[bh * a.M + row] = mg;
+  }
+}
+
+template <int KP>
+static hipError_t launch_rows_t(const RowsArgs& a, hipStream_t stream) {
+  const size_t lds = 4 * static_cast<size_t>(rows_wave_bytes(a.NB, KP));
+  if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+  auto kern = select_rows_kernel<KP>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds));
+  if (e != hipSuccess) return e;
+  const int64_t waves = static_cast<int64_t>(a.B) * a.H * a.nrows;
+  kern<<<dim3(static_cast<unsigned>((waves + 3) / 4)), 256, lds, stream>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_select_rows(const RowsArgs& a, hipStream_t stream) {
+  if (a.K <= 64) return launch_rows_t<64>(a, stream);
+  if (a.K <= 128) return launch_rows_t<128>(a, stream);
+  if (a.K <= 256) return launch_rows_t<256>(a, stream);
+  if (a.K <= 512) return launch_rows_t<512>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+template <int D, int P, int KP, bool STREAM, bool ROWS = false>
 static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                   const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                   float scaling, int k_base, int k_slots, int want_sigma,
                                   int32_t* kv_idx, float* sigma, float* tile_score,
-                                  const SelectDump& dump, hipStream_t stream) {
+                                  const SelectAux& aux, hipStream_t stream) {
   const int NB = (N + kBlock - 1) / kBlock;
   const int Qt = (M + kBlock - 1) / kBlock;
   const int grp = H / Hk;
@@ -617,15 +790,16 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   }
   if (W == 0 || 2 * L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
   const size_t lds = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(W) * L.wave_bytes;
-  const int64_t wgs = static_cast<int64_t>(B) * Hk * Qt * n_hc;
-  auto kern = select_kernel<D, P, KP, STREAM>;
+  const int tiles = ROWS ? aux.rows_t1 - aux.rows_t0 : Qt;
+  const int64_t wgs = static_cast<int64_t>(B) * Hk * tiles * n_hc;
+  auto kern = select_kernel<D, P, KP, STREAM, ROWS>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds));
   if (e != hipSuccess) return e;
   kern<<<dim3(static_cast<unsigned>(wgs)), 64 * W, lds, stream>>>(
       q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, n_hc, scaling, k_base,
-      k_slots, want_sigma, kv_idx, sigma, tile_score, dump);
+      k_slots, want_sigma, kv_idx, sigma, tile_score, aux);
   return hipGetLastError();
 }
 
@@ -634,7 +808,12 @@ static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h
                                    const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                    float scaling, int k_base, int k_slots, int want_sigma,
                                    int32_t* kv_idx, float* sigma, float* tile_score,
-                                   const SelectDump& dump, hipStream_t stream) {
+                                   const SelectAux& aux, hipStream_t stream) {
+  // per-row scores only: the smallest LDS layout (no row, no top-k)
+  if (aux.row_scores != nullptr)
+    return launch_select_t<D, P, 64, true, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,
+                                                 scaling, 1, 1, 0, nullptr, nullptr, nullptr, aux,
+                                                 stream);
   // rows of more than kStreamBlocks blocks stream their candidates, so that
   // LDS per wave does not grow with the context
   const bool stream_rows = (N + kBlock - 1) / kBlock > kStreamBlocks;
@@ -642,10 +821,10 @@ static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h
   return stream_rows                                                                        \
              ? launch_select_t<D, P, KP_, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, \
                                                 scaling, k_base, k_slots, want_sigma, kv_idx,  \
-                                                sigma, tile_score, dump, stream)               \
+                                                sigma, tile_score, aux, stream)                 \
              : launch_select_t<D, P, KP_, false>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,  \
                                                  scaling, k_base, k_slots, want_sigma, kv_idx, \
-                                                 sigma, tile_score, dump, stream)
+                                                 sigma, tile_score, aux, stream)
   if (k_slots <= 64) UGBSA_SEL(64);
   if (k_slots <= 128) UGBSA_SEL(128);
   if (k_slots <= 256) UGBSA_SEL(256);
@@ -658,9 +837,9 @@ hipError_t launch_select(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t 
                          const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
                          int mode, float scaling, int k_base, int k_slots, int want_sigma,
                          int32_t* kv_idx, float* sigma, float* tile_score,
-                         hipStream_t stream, const SelectDump* dump) {
-  const SelectDump off{};
-  const SelectDump& dm = dump != nullptr ? *dump : off;
+                         hipStream_t stream, const SelectAux* aux) {
+  const SelectAux off{};
+  const SelectAux& dm = aux != nullptr ? *aux : off;
 #define UGBSA_SELD(D_, P_)                                                                 \
   return launch_select_kp<D_, P_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,    \
                                   k_base, k_slots, want_sigma, kv_idx, sigma, tile_score,  \

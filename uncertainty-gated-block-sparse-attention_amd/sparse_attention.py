@@ -26,8 +26,14 @@ Differences from the reference, by design:
 * The dispatcher hands the selector and the kernel the un-repeated
   ``[B, Hk, N, D]`` key/value tensors (GQA handled in-kernel) instead of
   ``repeat_kv`` copies; ``_block_select_kv_idx_v2`` accepts either.
-* The v1 per-row path (``kernel_v2=False`` and the belief / rollout modes) is
-  not part of this build and raises ``NotImplementedError``.
+* The v1 per-row path (``kernel_v2=False``, and the belief / rollout modes)
+  runs on the GPU too: ``_block_select_mask`` (:208-382) through
+  ``ugbsa_select_mask`` + ``ugbsa_router_rows`` and ``block_sparse_attn``
+  through ``ugbsa_attn_fwd_rows``.  Its keep mask follows the same total tie
+  order, so rows with fewer visible blocks than the budget keep the lowest
+  invisible blocks (the reference keeps arbitrary ones; attention never
+  reads them).  ``rollout_peek`` (a depth-1 forward of the model per
+  candidate set) is not built and raises ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -38,7 +44,7 @@ import torch
 import torch.nn.functional as F
 
 import _capi
-from block_attn import attn_workspace, block_sparse_attn_v2
+from block_attn import attn_workspace, block_sparse_attn, block_sparse_attn_v2
 
 BLOCK = 64   # tokens per selection block (src/sparse_attention.py:51)
 
@@ -254,6 +260,135 @@ def _block_select_kv_idx_v2(query, key_states, scaling, block_m=64):
     return kv_idx
 
 
+@dataclass
+class MaskResult:
+    keep: torch.Tensor                     # bool [B, H, M, NB]
+    k_bud: int
+    margin: torch.Tensor | None = None     # fp32 [B, H, M] per-cell margin (router)
+    margin_eff: torch.Tensor | None = None  # after the row-grain mean
+    uncertain: torch.Tensor | None = None  # uint8 [B, H, M]
+    threshold: torch.Tensor | None = None  # fp32 [1]
+    scores: torch.Tensor | None = None     # fp32 [B, H, M, NB] ranked scores (if asked)
+
+
+# Largest per-pass row-score buffer of the v1 selector (fp32 elements, 1 GiB).
+_V1_WORKSPACE_ELEMS = 1 << 28
+
+
+def select_mask_v1(query, key_states, scaling, sel: Selector = None, want_scores=False,
+                   layer_idx=None) -> MaskResult:
+    """v1 per-row selection on the GPU: keep [B, H, M, NB] bool plus the router state.
+
+    src/sparse_attention.py:208-371 (kernels ``ugbsa_select_mask`` and
+    ``ugbsa_router_rows``); the rollout history lives in ``sel.selection_history``
+    ([H, NB] fp32 on the device) as in the reference.  Needs M == N (one-shot
+    prefill, as the reference's kernel assumes).
+    """
+    sel = SEL if sel is None else sel
+    assert query.is_cuda and query.dtype == torch.bfloat16, "bf16 HIP query required"
+    assert key_states.dtype == torch.bfloat16 and key_states.device == query.device
+    B, H, M, D = query.shape
+    Hk, N = key_states.shape[1], key_states.shape[2]
+    assert key_states.shape[0] == B and key_states.shape[3] == D and H % Hk == 0
+    assert M == N, "the per-row selector needs Q == K (one-shot prefill)"
+    dev = query.device
+    lib = _capi.lib()
+    stream = _capi.stream_ptr(dev)
+    query = _contig_rows(query)
+    nb = (N + BLOCK - 1) // BLOCK
+    mode = _capi.MODE_QUEST if use_quest(sel) else _capi.MODE_MEAN
+    planes = block_summary(key_states, mode)
+    if mode == _capi.MODE_MEAN and M > 1 and layer_idx is not None:
+        # the mean K of each block, repeat_kv'd, cached for later planners (:230-232)
+        kp = planes.view(B, Hk, nb, 3, D).float().sum(3).repeat_interleave(H // Hk, dim=1)
+        sel.k_pool_at[layer_idx] = kp.to(query.dtype)
+    k_bud = min(int(max(min(sel.k_max, sel.budget_blocks), sel.k_min)), nb)
+    router = sel.mode == "router"
+    k_eff = max(1, min(int(sel.budget_blocks), nb - 1)) if router else 0
+    belief = sel.mode not in ("topk", "router", "rollout", "quest")
+    penalty = None
+    if sel.mode == "rollout":
+        if sel.selection_history is None or tuple(sel.selection_history.shape) != (H, nb):
+            sel.selection_history = torch.zeros(H, nb, dtype=torch.float32, device=dev)
+        penalty = (float(sel.explore_bonus) * sel.selection_history.float()).contiguous()
+    per_tile = B * H * 64 * nb
+    full = lib.ugbsa_select_mask_workspace_elems(B, H, M, N)
+    ws_elems = full if want_scores else min(full, max(per_tile, _V1_WORKSPACE_ELEMS // per_tile * per_tile))
+    ws = torch.empty(ws_elems, dtype=torch.float32, device=dev)
+    keep = torch.empty(B, H, M, nb, dtype=torch.bool, device=dev)
+    margin = torch.empty(B, H, M, dtype=torch.float32, device=dev) if router else None
+    k_eff_kernel = k_eff if (router and nb > 1) else 0
+    _capi.check(lib.ugbsa_select_mask(query.data_ptr(), *query.stride(), planes.data_ptr(),
+                                      B, H, Hk, M, N, D, _capi.DTYPE_BF16, mode, float(scaling),
+                                      _capi.V1_BELIEF if belief else _capi.V1_TOPK, k_bud,
+                                      k_eff_kernel, int(sel.k_min), int(sel.k_max),
+                                      float(sel.top_p), _capi.ptr(penalty), ws.data_ptr(),
+                                      ws_elems, keep.data_ptr(), _capi.ptr(margin), stream),
+                "select_mask")
+    res = MaskResult(keep, k_bud, margin=margin)
+    if want_scores:
+        res.scores = ws.view(B, H, -1, nb)[:, :, :M]
+    if sel.mode == "rollout":
+        # EMA of the last row's selection after forcing (:291-295)
+        last = keep[0, :, -1, :].float()
+        sel.selection_history = ((1.0 - sel.ema_alpha) * sel.selection_history
+                                 + sel.ema_alpha * last)
+    if router:
+        res.margin_eff = torch.empty_like(margin)
+        res.uncertain = torch.empty(B, H, M, dtype=torch.uint8, device=dev)
+        res.threshold = torch.empty(1, dtype=torch.float32, device=dev)
+        if nb > 1:
+            grain = _capi.GRAIN_ROW if sel.router_grain == "row" else _capi.GRAIN_CELL
+            rmode = _capi.ROUTER_QUANTILE if sel.router_mode == "quantile" else _capi.ROUTER_ABS
+            # rows with more than k_eff visible blocks are eligible (:318-319);
+            # n_elig counts rows for row grain and cells for cell grain (:335-336)
+            elig_rows = max(0, M - 64 * k_eff)
+            n_elig = elig_rows if grain == _capi.GRAIN_ROW else B * H * elig_rows
+            k_quant = max(1, int(float(sel.router_quantile) * n_elig)) if n_elig > 0 else 0
+            _capi.check(lib.ugbsa_router_rows(margin.data_ptr(), B, H, M, nb, grain, rmode,
+                                              float(sel.router_tau), k_quant, k_eff,
+                                              keep.data_ptr(), res.margin_eff.data_ptr(),
+                                              res.uncertain.data_ptr(), res.threshold.data_ptr(),
+                                              stream),
+                        "router_rows")
+        else:
+            # a single block: the only score is both s_top and s_k, so every
+            # margin is 0 and no row is eligible
+            margin.zero_()
+            res.margin_eff.zero_()
+            res.uncertain.zero_()
+            res.threshold.fill_(float("nan"))
+    return res
+
+
+def _block_select_mask(query, key_states, scaling, layer_idx):
+    """v1 selection: keep [B, H, Q, NB] bool, built on the GPU.
+
+    Same contract as src/sparse_attention.py:208-382 (``key_states`` may be
+    repeat_kv'd or GQA), including the ``SEL.log`` diagnostics (:355-380).
+    """
+    res = select_mask_v1(query, key_states, scaling, layer_idx=layer_idx)
+    keep = res.keep
+    if SEL.log:
+        if res.uncertain is not None:
+            trig = float(res.uncertain.float().mean().item())
+            SEL.router_trigger_rate.append(trig)
+            SEL.router_eff_budget.append(float(keep.float().sum(dim=-1).mean().item()))
+            SEL.router_margin_mean.append(float(res.margin.mean().item()))
+            n_layers = len(SEL.model_ref.model.layers) if SEL.model_ref is not None else 0
+            if query.shape[-2] > 1 and n_layers and layer_idx == n_layers - 1:
+                tr = sum(SEL.router_trigger_rate) / len(SEL.router_trigger_rate)
+                eb = sum(SEL.router_eff_budget) / len(SEL.router_eff_budget)
+                mg = sum(SEL.router_margin_mean) / len(SEL.router_margin_mean)
+                knob = (f"q={SEL.router_quantile:.2f}" if SEL.router_mode == "quantile"
+                        else f"tau={SEL.router_tau:.3f}")
+                print(f"  router[{SEL.router_mode}/{SEL.router_grain}]: trigger={tr:.3f} "
+                      f"eff_budget={eb:.1f} margin={mg:.3f} {knob}", flush=True)
+        SEL.kept_blocks[layer_idx] = keep[0, :, -1, :].any(dim=0).cpu()
+        SEL.budget_samples.append(keep[0, :, -1, :].sum(dim=-1).float().mean().item())
+    return keep
+
+
 def needle_hit_rate(needle_blocks) -> float:
     """Mean over logged layers of the fraction of ``needle_blocks`` kept for
     the last Q tile (union over heads), read from ``SEL.kept_blocks`` as the
@@ -270,11 +405,12 @@ def needle_hit_rate(needle_blocks) -> float:
 
 def block_sparse_attention(module, query, key, value, attention_mask,
                            scaling, dropout=0.0, **kwargs):
-    """HF attention function (src/sparse_attention.py:751-788).
+    """HF attention function (src/sparse_attention.py:751-806).
 
     query [B, H, S, D]; key / value [B, Hk, S, D] as transformers passes them
     (before repeat_kv).  Dense SDPA for ``mode == "dense"`` or decode (Q == 1);
-    the HIP v2 path for topk / router / quest with ``SEL.kernel_v2``.  Returns
+    the HIP v2 path for topk / router / quest with ``SEL.kernel_v2``; the HIP
+    v1 per-row path otherwise (:790-804).  Returns
     ``(attn_output [B, S, H, D] contiguous, None)``.
     """
     Q = query.shape[-2]
@@ -301,9 +437,17 @@ def block_sparse_attention(module, query, key, value, attention_mask,
         PROF.stop(ev)
         return out, None
 
-    raise NotImplementedError(
-        f"SEL.mode={SEL.mode!r} with kernel_v2={SEL.kernel_v2}: the v1 per-row "
-        "path is not built on MI355X; use kernel_v2=True with topk/router/quest")
+    if SEL.mode == "rollout_peek":
+        raise NotImplementedError(
+            "SEL.mode='rollout_peek' (a depth-1 model forward per candidate set) is not built "
+            "on MI355X; the per-row modes topk / quest / router / belief / rollout are")
+    keep = _block_select_mask(query, key, scaling, module.layer_idx)
+    B, _, S, D = query.shape
+    out = torch.empty(B, S, H, D, dtype=query.dtype, device=query.device)
+    ws = attn_workspace(B, Hk, key.shape[-2], D, query.device)
+    block_sparse_attn(query, key, value, keep, scale=scaling, block_n=BLOCK,
+                      out=out.transpose(1, 2), workspace=ws)
+    return out, None
 
 
 def _register():
