@@ -40,6 +40,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
                    help="target CPU work of the bounded baseline sample")
+    p.add_argument("--path", choices=("v2", "v1"), default="v2",
+                   help="v2: per-tile selection (the headline); v1: the per-row path "
+                        "(kernel_v2=False: per-row keep mask, keep-masked attention)")
     p.add_argument("--pmc-run", action="store_true",
                    help="untimed driver for rocprofv3 --pmc: --steps layers of the workload, "
                         "then two copies of a 1 GiB tensor (counter calibration)")
@@ -303,6 +306,65 @@ def pmc_run(cfg, steps, torch, synth, dev):
     print("pmc run done", flush=True)
 
 
+def run_v1(args, cfg, q, k, v, torch):
+    """The v1 per-row path on one layer (SEL.kernel_v2 = False,
+    src/sparse_attention.py:790-804): per-row selection + router
+    (select_mask_v1), keep -> kv_idx + row masks, keep-masked attention.
+    The compaction syncs once for MAX_KEPT, as the reference does."""
+    import sparse_attention as sa
+    from block_attn import attn_workspace, block_sparse_attn, keep_kv_idx
+    sel = sa.Selector()
+    for f, val in cfg.sel_fields().items():
+        setattr(sel, f, val)
+    B, H, S, D = q.shape
+    ws = attn_workspace(B, k.shape[1], S, D, q.device)
+    out = torch.empty_like(q)
+    state = {}
+
+    def step(ev=None):
+        rec = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
+        rec(0)
+        res = sa.select_mask_v1(q, k, cfg.scaling, sel=sel)
+        rec(1)
+        block_sparse_attn(q, k, v, res.keep, cfg.scaling, out=out, workspace=ws)
+        rec(2)
+        state["res"] = res
+
+    warm_clocks(step, torch)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    sel_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    res = state["res"]
+    kv, _, max_kept = keep_kv_idx(res.keep, 64, want_rowmask=False)
+    t = torch.arange(kv.shape[2], device=kv.device).view(1, 1, -1, 1)
+    visited = ((kv[..., :max_kept] < kv.shape[-1]) & (kv[..., :max_kept] <= t)).sum().item()
+    flops = float(visited) * 4.0 * 64 * 64 * D
+    return {
+        "metric": "v1 per-row sparse prefill ms/layer (kernel_v2=False); executed TFLOP/s",
+        "value": round(sel_ms + attn_ms, 4), "unit": "ms/layer", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sel_ms + attn_ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V with planted needle blocks, synth.make_layer_fast on the GPU)",
+        "config": {"workload": f"{cfg.name} shape, v1 {cfg.mode}-on-{cfg.router_score} "
+                               f"budget {cfg.budget_blocks} per row, q={cfg.router_quantile} "
+                               f"{cfg.router_grain}-grain", "seq_len": cfg.S, "global_batch": cfg.B},
+        "kernels_ms": {"select_rows_and_router": round(sel_ms, 4),
+                       "compaction_and_attention": round(attn_ms, 4)},
+        "max_kept": int(max_kept),
+        "mean_kept_per_row": round(float(res.keep.float().sum(-1).mean().item()), 2),
+        "trigger_rate": (round(float(res.uncertain.float().mean().item()), 4)
+                         if res.uncertain is not None else None),
+        "executed_tflop": round(flops / 1e12, 4),
+        "executed_tflops": round(flops / (attn_ms * 1e-3) / 1e12, 1),
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -321,6 +383,9 @@ def main():
     t_gen = time.perf_counter()
     q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
     gen_s = time.perf_counter() - t_gen
+    if args.path == "v1":
+        print(json.dumps(run_v1(args, cfg, q, k, v, torch)), flush=True)
+        return
     runner = LayerRunner(cfg, q, k, v)
     ms_step, per = run_layer_bench(runner, args.steps, args.warmup, torch)
     attn_flops = runner.attended_flops()
