@@ -1,0 +1,21 @@
+// Kernel 3 at head_dim 256: the pipelined attention kernel (attn_pipe.h)
+// with a 64-row tile split over two wavefronts of 32 rows (a 64-row O^T
+// alone would take 256 registers), Q staged in LDS and one K / V^T register
+// set per wave.
+#include "attn_pipe.h"
+
+namespace ugbsa {
+
+hipError_t launch_attn_pipe256(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                               const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                               const uint16_t* vt, const int32_t* kv_idx,
+                               const uint64_t* rowmask, int64_t si_b, int64_t si_h,
+                               int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
+                               int k_slots, float scale, uint16_t* out, int64_t so_b,
+                               int64_t so_h, int64_t so_m, hipStream_t stream) {
+  return launch_attn_pipe<256, 2, true, true>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
+                                           rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt,
+                                           k_slots, scale, out, so_b, so_h, so_m, stream);
+}
+
+}  // namespace ugbsa

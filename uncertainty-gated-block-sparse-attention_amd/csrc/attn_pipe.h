@@ -1,0 +1,506 @@
+// The software-pipelined attention kernel over per-tile kv_idx (64-row
+// tiles, one wavefront per tile), shared by the head_dim 64 / 128 build
+// (attn_fwd.hip) and the head_dim 256 build (attn_fwd256.hip, compiled with
+// MFMA accumulators in AGPRs).
+#pragma once
+
+#include "common.h"
+#include "launch.h"
+
+namespace ugbsa {
+
+// Software-pipelined variant for 64-row tiles, one wavefront per tile.
+//
+// The visited blocks are processed as 32-key half blocks u = 0, 1, ...
+// (online softmax is exact at any key granularity).  Step u overlaps
+//   phase 1  MFMA: S^T(u+1) = K(u+1) . Q^T     ||  VALU: P(u) = exp2(S(u) - m),
+//                                                   row sums, bf16 packing
+//   phase 2  MFMA: O^T += V^T(u) . P^T(u)      ||  VALU: lane max of S(u+1)
+//                                                   and the lazy-offset test
+// with the VALU work woven between the MFMAs by hand.  The exp2 offsets m
+// are lazy (kLazyLog2) and tested lane-locally; the cross-lane row max and
+// the rescale of l and O run only when an offset must move, which after the
+// first blocks is rare.  K and V^T operands are prefetched into registers
+// two half blocks ahead (K(u+3) is requested after phase 1, V^T(u+2) after
+// phase 2); the two S, K and V register sets alternate between consecutive
+// steps (the loop is unrolled by 2).  Half blocks keep the live set at about
+// 430 registers: O^T 128, two S 64, P 16, Q 64, two K 64, two V^T 64.
+// Head_dim 256 (QLDS, SB) doubles O^T, K and V^T, so Q moves to LDS and K /
+// V^T keep one set each, requested one phase ahead.  The
+// tile's kv_idx row is compacted into LDS once (visited blocks only), so
+// sentinel and invisible slots cost nothing in the loop.
+// Per-wave LDS bytes of attn_fwd_pipe_kernel: Q fragments (QLDS), block
+// list, bitmap words and (with row masks) one mask per listed slot.
+__host__ __device__ inline int pipe_wave_lds(int D, int NT, bool qlds, int k_slots, int NB,
+                                             bool rowmask) {
+  const int words = (NB + 31) / 32;
+  int bytes = rowmask ? ((k_slots + words + 1) & ~1) * 4 + k_slots * 8 : (k_slots + words) * 4;
+  if (qlds) bytes += NT * (D / 32) * 64 * 16;
+  return (bytes + 15) / 16 * 16;
+}
+
+template <int D, int NT, bool QLDS, bool SB>
+__global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
+    const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+    const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+    const uint16_t* __restrict__ vt, const int32_t* __restrict__ kv_idx,
+    const uint64_t* __restrict__ rowmask, int64_t si_b, int64_t si_h, int64_t si_t, int B,
+    int Hk, int M, int N, int NB, int Qt, int k_slots, float scale_log2,
+    uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m, int units, int grp) {
+  constexpr int KS = D / 32, DT = D / 16, BM = 64;
+  // NT = 4: one wavefront per 64-row tile; NT = 2: two wavefronts, 32 rows
+  // each, which run independently (each keeps its own copy of the list)
+  static_assert(NT == 4 || NT == 2, "a wavefront takes 64 or 32 rows of a tile");
+  const int wave = threadIdx.x >> 6;
+  // dynamic LDS per wave: [Q fragments (QLDS)] [block list] [bitmap] [row masks]
+  extern __shared__ __align__(16) unsigned char psm_all[];
+  unsigned char* psm = psm_all + wave * pipe_wave_lds(D, NT, QLDS, k_slots, NB, rowmask != nullptr);
+  constexpr int QBYTES = QLDS ? NT * KS * 64 * 16 : 0;
+  int32_t* blist = reinterpret_cast<int32_t*>(psm + QBYTES);
+
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7;
+  const int rest = wg >> 3;
+  const int jh = rest % grp;
+  const int unit = (rest / grp) * 8 + xcd;
+  if (unit >= units) return;
+  const int per_t = B * Hk;
+  const int t = Qt - 1 - unit / per_t;
+  const int b = (unit % per_t) / Hk;
+  const int g = (unit % per_t) % Hk;
+  const int h = g * grp + jh;
+  const int lane = threadIdx.x & 63;
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int rbase = wave * 16 * NT;                  // this wave's first row in the tile
+  const int row0 = t * BM + rbase;
+  const int q_last = t * BM + BM - 1;
+
+  // ---- visited blocks of this tile, compacted into LDS in ascending order ---
+  // (the heads of a KV group and neighbouring tiles then sweep shared blocks
+  // together, which keeps them in L2).  A block listed twice in a row keeps
+  // the slot order, so it is visited twice as the reference loop does.
+  const int64_t idx_off = b * si_b + h * si_h + t * si_t;
+  const int32_t* idx = kv_idx + idx_off;
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t* bits = reinterpret_cast<uint32_t*>(blist + k_slots);
+  const int n_words = (min(t, NB - 1) >> 5) + 1;     // visible blocks are <= t
+  // per-row keep masks of the visited blocks (bit r: tile row r keeps the
+  // block), listed beside blist; without them every row attends every block
+  const uint64_t* rmk = rowmask != nullptr ? rowmask + idx_off : nullptr;
+  uint64_t* mlist = reinterpret_cast<uint64_t*>(
+      blist + ((k_slots + (NB + 31) / 32 + 1) & ~1));
+  for (int w = lane; w < n_words; w += 64) bits[w] = 0u;
+  wave_lds_sync();
+  int nv = 0;
+  bool dup = false;
+  for (int base = 0; base < k_slots; base += 64) {
+    const int s = base + lane;
+    const int blk = s < k_slots ? idx[s] : -1;
+    const bool ok = blk >= 0 && blk < NB && blk * kBlock <= q_last;
+    const uint64_t bal = __ballot(ok);
+    if (ok) {
+      blist[nv + __popcll(bal & lt_mask)] = blk;
+      if (rmk != nullptr) mlist[nv + __popcll(bal & lt_mask)] = rmk[s];
+      const uint32_t bit = 1u << (blk & 31);
+      dup |= (atomicOr(&bits[blk >> 5], bit) & bit) != 0u;
+    }
+    nv += __popcll(bal);
+  }
+  wave_lds_sync();
+  // with row masks the slots are visited in their order (the masks are
+  // listed per slot); otherwise a list without repeats is re-sorted
+  if (rmk == nullptr && __ballot(dup) == 0) {
+    int pos = 0;
+    for (int w0 = 0; w0 < n_words; w0 += 64) {
+      const int w = w0 + lane;
+      uint32_t word = w < n_words ? bits[w] : 0u;
+      const uint32_t cnt = __popc(word);
+      int at = pos + static_cast<int>(wave_excl_scan(cnt, lane));
+      while (word) {
+        const int j = __ffs(word) - 1;
+        blist[at++] = w * 32 + j;
+        word &= word - 1u;
+      }
+      pos = __shfl(at, 63, 64);
+    }
+    wave_lds_sync();
+  }
+
+  // ---- Q tile: MFMA B operands held in registers ---------------------------
+  const uint16_t* qb = q + b * sq_b + h * sq_h;
+  bf16x8 qf[QLDS ? 1 : NT][QLDS ? 1 : KS];
+  // With QLDS the fragments are staged once in LDS in operand order —
+  // fragment (nt, ks) is one KiB with lane L's 16 bytes at 16 L — and read
+  // back one fragment per MFMA pair (ds_read_b128, conflict-free), which
+  // keeps Q (4 KS VGPRs a row set) out of the register file.
+  bf16x8* qs = reinterpret_cast<bf16x8*>(psm);
+  // A negative scale is moved onto Q (bf16 negation is exact), so the
+  // scores the softmax sees are always scaled by sl2 > 0.
+  const float sl2 = fabsf(scale_log2);
+  const uint32_t qsign = scale_log2 < 0.f ? 0x80008000u : 0u;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = row0 + 16 * nt + r16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 x = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4,
+                                     load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
+                               : zero_bf16x8();
+      if constexpr (QLDS) qs[(nt * KS + ks) * 64 + lane] = x;
+      else qf[nt][ks] = x;
+    }
+  }
+  if constexpr (QLDS) wave_lds_sync();
+  auto qfrag = [&](int nt, int ks) -> bf16x8 {
+    if constexpr (QLDS) return qs[(nt * KS + ks) * 64 + lane];
+    else return qf[nt][ks];
+  };
+
+  // K and V^T operands of this KV head, in load order (kv_operand_kernel):
+  // half block (blk, half) = K slabs at ((2 blk + half) * 2 * KS) KiB and
+  // V^T slabs at ((2 blk + half) * DT) KiB; lane L reads 16 bytes at 16 L.
+  const int64_t head_elems = static_cast<int64_t>(NB) * kBlock * D;
+  const int64_t part = static_cast<int64_t>(B) * Hk * head_elems;
+  const uint16_t* kop_head = vt + (static_cast<int64_t>(b) * Hk + g) * head_elems;
+  const uint16_t* vop_head = kop_head + part;
+  const int nu = 2 * nv;
+
+  typedef bf16x8 KSet[2][KS];
+  typedef bf16x8 VSet[DT];
+  typedef f32x4 SBuf[2][NT];
+  // Half block u (clamped to the last one) -> its block id (LDS read; the
+  // caller applies readfirstlane where it needs the id, so the read can be
+  // issued early) and its half.
+  auto clamp_u = [&](int u) -> int { return min(u, nu - 1); };
+  auto blk_raw = [&](int u) -> int { return blist[clamp_u(u) >> 1]; };
+  auto uni = [](int x) -> int { return __builtin_amdgcn_readfirstlane(x); };
+  // Global (not buffer) loads: a wavefront streams K/V through the vector
+  // memory pipeline faster with them, and every visited block lies inside
+  // the operand copy, so no range check is needed.
+  auto load_k = [&](int blk, int half, KSet& kf) {
+    const uint16_t* p = kop_head + static_cast<int64_t>(2 * blk + half) * (2 * KS * 512) + lane * 8;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = load_bf16x8(p + (mt * KS + ks) * 512);
+  };
+  auto load_v = [&](int blk, int half, VSet& vf) {
+    const uint16_t* p = vop_head + static_cast<int64_t>(2 * blk + half) * (DT * 512) + lane * 8;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vf[dt] = load_bf16x8(p + dt * 512);
+  };
+
+  f32x4 o[DT][NT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[NT], l[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; }
+  bf16x8 pb[NT];
+
+  // Row-keep mask of half block u (wave-uniform), all rows without masks.
+  auto mbits = [&](int u) -> uint64_t {
+    if (rmk == nullptr) return ~0ull;
+    const uint64_t x = mlist[clamp_u(u) >> 1];
+    return (static_cast<uint64_t>(uni(static_cast<int>(x >> 32))) << 32) |
+           static_cast<uint32_t>(uni(static_cast<int>(x)));
+  };
+  // Causal / bounds / row-keep mask (only half blocks crossing the diagonal
+  // or N, or not kept by every row).
+  auto mask = [&](SBuf& st, int blk, int half, uint64_t mk) {
+    const int kbase = blk * kBlock + 32 * half;
+    if ((kbase + 31 > row0) || (kbase + 32 > N) || mk != ~0ull) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = row0 + 16 * nt + r16;
+        const bool off = ((mk >> (rbase + 16 * nt + r16)) & 1ull) == 0;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kbase + 8 * g4 + 4 * mt + i;
+            if (off || key > row || key >= N) st[mt][nt][i] = -INFINITY;
+          }
+      }
+    }
+  };
+  // Lazy offsets, tested lane-locally: a row's offset m only moves when some
+  // lane's max of its raw scores exceeds thr = (m + kLazyLog2) / sl2; the
+  // cross-lane row max is only formed inside the (rare) rescale.
+  float thr[NT], rm[NT], tm[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) thr[nt] = -INFINITY;
+  const float inv_sl2 = 1.0f / sl2;
+  // +inf in a register the optimiser cannot see through: med3(a, b, +inf) is
+  // max(a, b) without the canonicalising copies that fmaxf of MFMA results
+  // gets in IEEE mode.
+  float pinf = INFINITY;
+  asm volatile("" : "+v"(pinf));
+  auto mx2 = [&](float a, float b) -> float { return __builtin_amdgcn_fmed3f(a, b, pinf); };
+  bool grow = false;
+  // Row-max unit r of S (nt = r / 4): stages 0-2 the max tree of the lane's
+  // eight values, stage 3 the test against thr.
+  auto rowmax_unit = [&](const SBuf& st, int r) {
+    const int nt = r / 4, stage = r % 4;
+    if (stage == 0) {
+      tm[nt][0] = mx2(st[0][nt][0], st[0][nt][1]);
+      tm[nt][1] = mx2(st[0][nt][2], st[0][nt][3]);
+    } else if (stage == 1) {
+      tm[nt][2] = mx2(st[1][nt][0], st[1][nt][1]);
+      tm[nt][3] = mx2(st[1][nt][2], st[1][nt][3]);
+    } else if (stage == 2) {
+      tm[nt][0] = mx2(tm[nt][0], tm[nt][1]);
+      tm[nt][2] = mx2(tm[nt][2], tm[nt][3]);
+    } else {
+      rm[nt] = mx2(tm[nt][0], tm[nt][2]);
+      grow |= rm[nt] > thr[nt];
+    }
+  };
+  // Move the offsets to the new row maxima (lane maxima rm -> row maxima)
+  // and rescale l and O.
+  auto rescale = [&]() {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float m_new = fmaxf(m[nt], quad_rows_max(rm[nt]) * sl2);
+      const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_new);
+      m[nt] = m_new;
+      thr[nt] = (m_new + kLazyLog2) * inv_sl2;
+      l[nt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= alpha;
+    }
+  };
+  // Softmax element e of S (nt = e / 8): P = exp2(S * sl2 - m), the row sum
+  // and the bf16 packing of P into pb.
+  float p[NT][8], sum[NT];
+  uint32_t w[NT][4];
+  auto softmax_elem = [&](const SBuf& st, int e) {
+    const int nt = e / 8, kk = e % 8, mt = kk / 4, i = kk % 4;
+    p[nt][kk] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], sl2, -m[nt]));
+    sum[nt] = kk == 0 ? p[nt][0] : sum[nt] + p[nt][kk];
+    if (kk & 1) w[nt][kk / 2] = cvt_pk_bf16(p[nt][kk - 1], p[nt][kk]);
+    if (kk == 7) {
+      l[nt] += sum[nt];
+      pb[nt] = __builtin_bit_cast(bf16x8, u32x4{w[nt][0], w[nt][1], w[nt][2], w[nt][3]});
+    }
+  };
+  // S^T of one half block without interleaved work (prologue).
+  auto qk = [&](SBuf& st, const KSet& kf) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          st[mt][nt] = mfma16x16x32(kf[mt][ks], qfrag(nt, ks), ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[mt][nt]);
+  };
+
+  // The two phases of a step are woven by hand (one wave per SIMD issues in
+  // order, so VALU work has to sit between the MFMAs of the instruction
+  // stream); sched_barrier keeps the compiler from regrouping them.
+  //   phase 1: S^T(u+1) (NM1 MFMAs) || softmax of S(u) (32 elements a lane)
+  //   phase 2: O^T += V^T P^T(u) (NM2 MFMAs) || the row-max test of S(u+1)
+  constexpr int NM1 = 2 * NT * KS, P1 = NM1 / 2;
+  constexpr int EPP = 8 * NT / P1;                  // softmax elements per MFMA pair
+  constexpr int NM2 = DT * NT, P2 = NM2 / 2;
+  constexpr int RU = 4 * NT;                        // row-max units, spread over the P2 pairs
+  static_assert(EPP * P1 == 8 * NT, "phase work must split evenly");
+  auto phase1 = [&](const SBuf& cur, SBuf& nxt, const KSet& kf) {
+    if constexpr (QLDS) {
+      // pair j = (ks, nt): both M-tiles of fragment (nt, ks); the fragment
+      // of pair j + 2 is requested in pair j, two MFMA pairs ahead of use
+      bf16x8 qr[3];
+      qr[0] = qfrag(0, 0);
+      qr[1] = qfrag(1 % NT, 1 / NT);
+      static_for<P1>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int ks = j / NT, nt = j % NT;
+        if constexpr (j + 2 < P1) qr[(j + 2) % 3] = qfrag((j + 2) % NT, (j + 2) / NT);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qr[j % 3],
+                                     ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
+#pragma unroll
+        for (int e = j * EPP; e < (j + 1) * EPP; ++e) softmax_elem(cur, e);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    } else {
+#pragma unroll
+      for (int j = 0; j < P1; ++j) {
+#pragma unroll
+        for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
+          const int ks = jj / (2 * NT), mt = (jj / NT) & 1, nt = jj % NT;
+          nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
+        }
+#pragma unroll
+        for (int e = j * EPP; e < (j + 1) * EPP; ++e) softmax_elem(cur, e);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  auto phase2 = [&](const SBuf& nx, const VSet& vf) -> bool {
+    grow = false;
+#pragma unroll
+    for (int j = 0; j < P2; ++j) {
+#pragma unroll
+      for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
+        const int dt = jj / NT, nt = jj % NT;
+        o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+      }
+#pragma unroll
+      for (int r = (j * RU + P2 - 1) / P2; r < ((j + 1) * RU + P2 - 1) / P2; ++r) rowmax_unit(nx, r);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return __ballot(grow) != 0;
+  };
+  auto rowmax = [&](const SBuf& st) -> bool {
+    grow = false;
+#pragma unroll
+    for (int r = 0; r < 4 * NT; ++r) rowmax_unit(st, r);
+    return __ballot(grow) != 0;
+  };
+  // Softmax and P.V of the last half block (epilogue, not woven).
+  auto softmax = [&](const SBuf& st) {
+#pragma unroll
+    for (int e = 0; e < 8 * NT; ++e) softmax_elem(st, e);
+  };
+  auto pv = [&](const VSet& vf) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+  };
+
+  SBuf sa, sb;
+  KSet ka, kb;
+  VSet va, vb;
+  if constexpr (SB) {
+    // One K and one V^T set (head_dim 256: two would take 256 registers).
+    // Step u: S(u) in cur, K(u+1) in ka, V(u) in va; K(u+2) is requested
+    // after phase 1 and V(u+1) after phase 2 — a phase ahead of use, which
+    // at this head_dim is about 2000 cycles.
+    auto step1 = [&](SBuf& cur, SBuf& nxt, int u) {
+      const int rk = blk_raw(u + 2), rm1 = blk_raw(u + 1);
+      phase1(cur, nxt, ka);
+      load_k(uni(rk), clamp_u(u + 2) & 1, ka);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        u32x4 pin = __builtin_bit_cast(u32x4, pb[nt]);
+        asm volatile("" : "+v"(pin), "+v"(l[nt]));
+        pb[nt] = __builtin_bit_cast(bf16x8, pin);
+      }
+      mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
+      const bool moved = phase2(nxt, va);
+      load_v(uni(rm1), (u + 1) & 1, va);
+      if (moved) rescale();
+    };
+    if (nv > 0) {
+      load_k(uni(blk_raw(0)), 0, ka);
+      load_v(uni(blk_raw(0)), 0, va);
+      qk(sa, ka);
+      load_k(uni(blk_raw(1)), clamp_u(1) & 1, ka);
+      mask(sa, uni(blk_raw(0)), 0, mbits(0));
+      if (rowmax(sa)) rescale();
+      int u = 0;
+      for (; u + 2 <= nu - 2; u += 2) {
+        step1(sa, sb, u);
+        step1(sb, sa, u + 1);
+      }
+      step1(sa, sb, u);
+      softmax(sb);
+      pv(va);
+    }
+  }
+  // Step u: S(u) in cur, K(u+1) in kc, V(u) in vc; K(u+2) / V(u+1) in flight.
+  auto step = [&](SBuf& cur, SBuf& nxt, KSet& kc, VSet& vc, int u) {
+    // block ids of K(u+3), the mask of S(u+1) and V(u+2), read from LDS
+    // before phase 1 so that their latency hides behind it
+    const int rk = blk_raw(u + 3), rm1 = blk_raw(u + 1), rv = blk_raw(u + 2);
+    phase1(cur, nxt, kc);
+    load_k(uni(rk), clamp_u(u + 3) & 1, kc);
+    // P and the row sums are only read later; pin them so that their
+    // computation is not sunk past the mask branch into phase 2
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      u32x4 pin = __builtin_bit_cast(u32x4, pb[nt]);
+      asm volatile("" : "+v"(pin), "+v"(l[nt]));
+      pb[nt] = __builtin_bit_cast(bf16x8, pin);
+    }
+    mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
+    const bool moved = phase2(nxt, vc);
+    load_v(uni(rv), clamp_u(u + 2) & 1, vc);
+    if (moved) rescale();
+  };
+
+  if (!SB && nv > 0) {
+    load_k(uni(blk_raw(0)), 0, ka);
+    load_k(uni(blk_raw(1)), 1, kb);
+    load_v(uni(blk_raw(0)), 0, va);
+    load_v(uni(blk_raw(1)), 1, vb);
+    qk(sa, ka);
+    load_k(uni(blk_raw(2)), clamp_u(2) & 1, ka);
+    mask(sa, uni(blk_raw(0)), 0, mbits(0));
+    if (rowmax(sa)) rescale();
+    // nu = 2 * nv is even: steady steps u = 0 .. nu - 2, then the last half block.
+    int u = 0;
+    for (; u + 2 <= nu - 2; u += 2) {
+      step(sa, sb, kb, va, u);
+      step(sb, sa, ka, vb, u + 1);
+    }
+    step(sa, sb, kb, va, u);
+    softmax(sb);
+    pv(vb);
+  }
+
+  // ---- normalise and store ------------------------------------------------
+  uint16_t* ob = out + b * so_b + h * so_h;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float lt = l[nt];
+    lt = quad_rows_sum(lt);
+    const float inv = lt > 0.f ? 1.0f / lt : 1.0f;
+    const int row = row0 + 16 * nt + r16;
+    if (row < M) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint32_t w0 = cvt_pk_bf16(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
+        const uint32_t w1 = cvt_pk_bf16(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
+        *reinterpret_cast<uint2*>(ob + row * so_m + 16 * dt + 4 * g4) = make_uint2(w0, w1);
+      }
+    }
+  }
+}
+
+template <int D, int NT, bool QLDS, bool SB>
+static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                                   const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                                   const uint16_t* vt, const int32_t* kv_idx,
+                                   const uint64_t* rowmask, int64_t si_b, int64_t si_h,
+                                   int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
+                                   int k_slots, float scale, uint16_t* out, int64_t so_b,
+                                   int64_t so_h, int64_t so_m, hipStream_t stream) {
+  const int NB = (N + kBlock - 1) / kBlock;
+  const int grp = H / Hk;
+  const int units = B * Hk * Qt;
+  const int64_t wgs = 8LL * grp * ((units + 7) / 8);
+  constexpr int WPT = 4 / NT;
+  const size_t lds = static_cast<size_t>(WPT) *
+                     pipe_wave_lds(D, NT, QLDS, k_slots, NB, rowmask != nullptr);
+  if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+  auto kern = attn_fwd_pipe_kernel<D, NT, QLDS, SB>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
+  kern<<<dim3(static_cast<unsigned>(wgs)), 64 * WPT, lds, stream>>>(
+      q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, Hk, M,
+      N, NB, Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
+  return hipGetLastError();
+}
+
+
+}  // namespace ugbsa
