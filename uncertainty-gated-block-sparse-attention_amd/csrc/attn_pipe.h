@@ -1,7 +1,7 @@
 // The software-pipelined attention kernel over per-tile kv_idx (64-row
-// tiles, one wavefront per tile), shared by the head_dim 64 / 128 build
-// (attn_fwd.hip) and the head_dim 256 build (attn_fwd256.hip, compiled with
-// MFMA accumulators in AGPRs).
+// tiles), shared by the head_dim 64 / 128 build (attn_fwd.hip, one
+// wavefront per tile) and the head_dim 256 build (attn_fwd256.hip, two
+// wavefronts of 32 rows per tile).
 #pragma once
 
 #include "common.h"
@@ -9,25 +9,27 @@
 
 namespace ugbsa {
 
-// Software-pipelined variant for 64-row tiles, one wavefront per tile.
-//
 // The visited blocks are processed as 32-key half blocks u = 0, 1, ...
-// (online softmax is exact at any key granularity).  Step u overlaps
-//   phase 1  MFMA: S^T(u+1) = K(u+1) . Q^T     ||  VALU: P(u) = exp2(S(u) - m),
-//                                                   row sums, bf16 packing
-//   phase 2  MFMA: O^T += V^T(u) . P^T(u)      ||  VALU: lane max of S(u+1)
-//                                                   and the lazy-offset test
-// with the VALU work woven between the MFMAs by hand.  The exp2 offsets m
-// are lazy (kLazyLog2) and tested lane-locally; the cross-lane row max and
-// the rescale of l and O run only when an offset must move, which after the
-// first blocks is rare.  K and V^T operands are prefetched into registers
-// two half blocks ahead (K(u+3) is requested after phase 1, V^T(u+2) after
-// phase 2); the two S, K and V register sets alternate between consecutive
-// steps (the loop is unrolled by 2).  Half blocks keep the live set at about
-// 430 registers: O^T 128, two S 64, P 16, Q 64, two K 64, two V^T 64.
-// Head_dim 256 (QLDS, SB) doubles O^T, K and V^T, so Q moves to LDS and K /
-// V^T keep one set each, requested one phase ahead.  The
-// tile's kv_idx row is compacted into LDS once (visited blocks only), so
+// (online softmax is exact at any key granularity).  At head_dim 64 / 128
+// step u overlaps
+//   phase 1  MFMA: S^T(u+1) = K(u+1) . Q^T     ||  VALU: second half of
+//                                                   P(u) = exp2(S(u) - m)
+//   phase 2  MFMA: O^T += V^T(u) . P^T(u)      ||  VALU: first half of P(u+1)
+// (row sums and bf16 packing included), with the VALU work woven between the
+// MFMAs by hand.  The exp2 offsets m are lazy (kLazyLog2): a half block's P
+// is computed with the current m, and only when some lane's sum of its P
+// values exceeds 2^kLazyLog2 (commit) are the row maxima formed, l and O
+// rescaled and P recomputed — after the first blocks a rare event.  K and
+// V^T operands are prefetched into registers two half blocks ahead (K(u+3)
+// is requested after phase 1, V^T(u+2) after phase 2); the two S, K and V
+// register sets alternate between consecutive steps (the loop is unrolled by
+// 2).  Half blocks keep the live set at about 470 registers: O^T 128, two S
+// 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K 64, two V^T 64.
+// Head_dim 256 (QLDS, SB) doubles O^T, K and V^T, so Q moves to LDS, K /
+// V^T keep one set each, requested one phase ahead, and phase 1 computes all
+// of P(u) while phase 2 forms the lane maxima of S(u+1) and tests them
+// against the lazy threshold (the rescale follows phase 2 when one moved).
+// The tile's kv_idx row is compacted into LDS once (visited blocks only), so
 // sentinel and invisible slots cost nothing in the loop.
 // Per-wave LDS bytes of attn_fwd_pipe_kernel: Q fragments (QLDS), block
 // list, bitmap words and (with row masks) one mask per listed slot.
@@ -146,8 +148,16 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       const bf16x8 x = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4,
                                      load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
                                : zero_bf16x8();
-      if constexpr (QLDS) qs[(nt * KS + ks) * 64 + lane] = x;
-      else qf[nt][ks] = x;
+      if constexpr (QLDS) {
+        qs[(nt * KS + ks) * 64 + lane] = x;
+      } else {
+        // Q lives in AGPRs for the whole tile: the MFMAs read their B
+        // operand from there, where a VGPR copy would be spilled to AGPRs
+        // and copied back (v_accvgpr_read) for every use
+        u32x4 xa = __builtin_bit_cast(u32x4, x);
+        asm volatile("" : "+a"(xa));
+        qf[nt][ks] = __builtin_bit_cast(bf16x8, xa);
+      }
     }
   }
   if constexpr (QLDS) wave_lds_sync();
@@ -226,9 +236,11 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       }
     }
   };
-  // Lazy offsets, tested lane-locally: a row's offset m only moves when some
-  // lane's max of its raw scores exceeds thr = (m + kLazyLog2) / sl2; the
-  // cross-lane row max is only formed inside the (rare) rescale.
+  // Lazy offsets at head_dim 256, tested lane-locally: a row's offset m only
+  // moves when some lane's max of its raw scores exceeds
+  // thr = (m + kLazyLog2) / sl2; the cross-lane row max is only formed inside
+  // the (rare) rescale.  Head_dim 64 / 128 tests the row sums instead
+  // (commit) and forms lane maxima only when that test fires.
   float thr[NT], rm[NT], tm[NT][4];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) thr[nt] = -INFINITY;
@@ -282,7 +294,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     sum[nt] = kk == 0 ? p[nt][0] : sum[nt] + p[nt][kk];
     if (kk & 1) w[nt][kk / 2] = cvt_pk_bf16(p[nt][kk - 1], p[nt][kk]);
     if (kk == 7) {
-      l[nt] += sum[nt];
+      if constexpr (SB) l[nt] += sum[nt];
       pb[nt] = __builtin_bit_cast(bf16x8, u32x4{w[nt][0], w[nt][1], w[nt][2], w[nt][3]});
     }
   };
@@ -300,13 +312,19 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // The two phases of a step are woven by hand (one wave per SIMD issues in
   // order, so VALU work has to sit between the MFMAs of the instruction
   // stream); sched_barrier keeps the compiler from regrouping them.
-  //   phase 1: S^T(u+1) (NM1 MFMAs) || softmax of S(u) (32 elements a lane)
+  // Head_dim 256 (SB):
+  //   phase 1: S^T(u+1) (NM1 MFMAs) || softmax of S(u) (all 8 NT elements)
   //   phase 2: O^T += V^T P^T(u) (NM2 MFMAs) || the row-max test of S(u+1)
+  // Head_dim 64 / 128:
+  //   phase 1: S^T(u+1) || softmax elements [4 NT, 8 NT) of S(u)
+  //   phase 2: O^T += V^T P^T(u) || softmax elements [0, 4 NT) of S(u+1)
+  // with the lazy test after phase 1, on the row sums (commit).
   constexpr int NM1 = 2 * NT * KS, P1 = NM1 / 2;
-  constexpr int EPP = 8 * NT / P1;                  // softmax elements per MFMA pair
+  constexpr int E1ST = SB ? 0 : 4 * NT;             // first softmax element of phase 1
+  constexpr int EPP = (8 * NT - E1ST) / P1;         // softmax elements per MFMA pair
   constexpr int NM2 = DT * NT, P2 = NM2 / 2;
   constexpr int RU = 4 * NT;                        // row-max units, spread over the P2 pairs
-  static_assert(EPP * P1 == 8 * NT, "phase work must split evenly");
+  static_assert(EPP * P1 == 8 * NT - E1ST, "phase work must split evenly");
   auto phase1 = [&](const SBuf& cur, SBuf& nxt, const KSet& kf) {
     if constexpr (QLDS) {
       // pair j = (ks, nt): both M-tiles of fragment (nt, ks); the fragment
@@ -323,7 +341,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
           nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qr[j % 3],
                                      ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
 #pragma unroll
-        for (int e = j * EPP; e < (j + 1) * EPP; ++e) softmax_elem(cur, e);
+        for (int e = E1ST + j * EPP; e < E1ST + (j + 1) * EPP; ++e) softmax_elem(cur, e);
         __builtin_amdgcn_sched_barrier(0);
       });
     } else {
@@ -335,7 +353,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
           nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
         }
 #pragma unroll
-        for (int e = j * EPP; e < (j + 1) * EPP; ++e) softmax_elem(cur, e);
+        for (int e = E1ST + j * EPP; e < E1ST + (j + 1) * EPP; ++e) softmax_elem(cur, e);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -371,6 +389,46 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+  };
+  // Phase 2 of head_dim 64 / 128: the P.V MFMAs row set by row set; once
+  // row set nt' of P(u) has been read, row set nt' of P(u+1) is computed
+  // (elements 8 nt' .. 8 nt' + 7 of S(u+1), over the next DT / 2 pairs).
+  auto phase2s = [&](const SBuf& nx, const VSet& vf) {
+    constexpr int PPN = DT / 2, EPN = 8 / PPN;
+    static_assert(PPN * (NT / 2 + 1) <= P2, "row sets of P(u+1) fit in phase 2");
+#pragma unroll
+    for (int j = 0; j < P2; ++j) {
+#pragma unroll
+      for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
+        const int nt = jj / DT, dt = jj % DT;
+        o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+      }
+      if (j >= PPN && j < PPN * (NT / 2 + 1)) {
+#pragma unroll
+        for (int e = (j - PPN) * EPN; e < (j - PPN + 1) * EPN; ++e) softmax_elem(nx, e);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // The lazy test of head_dim 64 / 128, after the softmax of half block st
+  // is complete: a lane's sum of its eight P values above 2^kLazyLog2 means
+  // the offset m of that row is stale (some P exceeded the lazy bound).
+  // Then the offsets move to the half block's row maxima, l and O are
+  // rescaled and the softmax is redone — rare, as each move raises m by more
+  // than kLazyLog2 - 3.  Otherwise every P is at most 2^kLazyLog2.  The row
+  // sums enter l only after the test.
+  const float big_sum = __builtin_exp2f(kLazyLog2);
+  auto commit = [&](const SBuf& st) {
+    bool big = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) big |= sum[nt] > big_sum;
+    if (__ballot(big) != 0) {
+      rowmax(st);
+      rescale();
+      softmax(st);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) l[nt] += sum[nt];
   };
 
   SBuf sa, sb;
@@ -419,6 +477,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     // before phase 1 so that their latency hides behind it
     const int rk = blk_raw(u + 3), rm1 = blk_raw(u + 1), rv = blk_raw(u + 2);
     phase1(cur, nxt, kc);
+    commit(cur);
     load_k(uni(rk), clamp_u(u + 3) & 1, kc);
     // P and the row sums are only read later; pin them so that their
     // computation is not sunk past the mask branch into phase 2
@@ -429,20 +488,24 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       pb[nt] = __builtin_bit_cast(bf16x8, pin);
     }
     mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
-    const bool moved = phase2(nxt, vc);
+    phase2s(nxt, vc);
     load_v(uni(rv), clamp_u(u + 2) & 1, vc);
-    if (moved) rescale();
   };
 
   if (!SB && nv > 0) {
+    // the loads are issued in the loop's order (K(u+1), V(u), K(u+2),
+    // V(u+1) outstanding at each step), so that the wait counts the compiler
+    // derives for the loop hold for its first iteration as for the others
     load_k(uni(blk_raw(0)), 0, ka);
     load_k(uni(blk_raw(1)), 1, kb);
     load_v(uni(blk_raw(0)), 0, va);
-    load_v(uni(blk_raw(1)), 1, vb);
     qk(sa, ka);
     load_k(uni(blk_raw(2)), clamp_u(2) & 1, ka);
+    load_v(uni(blk_raw(1)), 1, vb);
     mask(sa, uni(blk_raw(0)), 0, mbits(0));
     if (rowmax(sa)) rescale();
+#pragma unroll
+    for (int e = 0; e < E1ST; ++e) softmax_elem(sa, e);
     // nu = 2 * nv is even: steady steps u = 0 .. nu - 2, then the last half block.
     int u = 0;
     for (; u + 2 <= nu - 2; u += 2) {
@@ -450,7 +513,9 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       step(sb, sa, ka, vb, u + 1);
     }
     step(sa, sb, kb, va, u);
-    softmax(sb);
+#pragma unroll
+    for (int e = E1ST; e < 8 * NT; ++e) softmax_elem(sb, e);
+    commit(sb);
     pv(vb);
   }
 
