@@ -1,7 +1,7 @@
 // The software-pipelined attention kernel over per-tile kv_idx (64-row
-// tiles), shared by the head_dim 64 / 128 build (attn_fwd.hip, one
-// wavefront per tile) and the head_dim 256 build (attn_fwd256.hip, two
-// wavefronts of 32 rows per tile).
+// tiles), shared by the head_dim 64 / 128 builds (attn_fwd.hip and, for long
+// contexts, attn_fwd_long.hip; one wavefront per tile) and the head_dim 256
+// build (attn_fwd256.hip, two wavefronts of 32 rows per tile).
 #pragma once
 
 #include "common.h"
@@ -10,8 +10,8 @@
 namespace ugbsa {
 
 // The visited blocks are processed as 32-key half blocks u = 0, 1, ...
-// (online softmax is exact at any key granularity).  At head_dim 64 / 128
-// step u overlaps
+// (online softmax is exact at any key granularity).  Without SB (head_dim
+// 64 / 128) step u overlaps
 //   phase 1  MFMA: S^T(u+1) = K(u+1) . Q^T     ||  VALU: second half of
 //                                                   P(u) = exp2(S(u) - m)
 //   phase 2  MFMA: O^T += V^T(u) . P^T(u)      ||  VALU: first half of P(u+1)
@@ -25,10 +25,11 @@ namespace ugbsa {
 // register sets alternate between consecutive steps (the loop is unrolled by
 // 2).  Half blocks keep the live set at about 470 registers: O^T 128, two S
 // 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K 64, two V^T 64.
-// Head_dim 256 (QLDS, SB) doubles O^T, K and V^T, so Q moves to LDS, K /
-// V^T keep one set each, requested one phase ahead, and phase 1 computes all
-// of P(u) while phase 2 forms the lane maxima of S(u+1) and tests them
-// against the lazy threshold (the rescale follows phase 2 when one moved).
+// With SB (head_dim 256, and head_dim 128 for long contexts) K / V^T keep
+// one set each, requested one phase ahead, and phase 1 computes all of P(u)
+// while phase 2 forms the lane maxima of S(u+1) and tests them against the
+// lazy threshold (the rescale follows phase 2 when one moved).  Head_dim 256
+// (QLDS) doubles O^T, K and V^T, so Q moves to LDS.
 // The tile's kv_idx row is compacted into LDS once (visited blocks only), so
 // sentinel and invisible slots cost nothing in the loop.
 // Per-wave LDS bytes of attn_fwd_pipe_kernel: Q fragments (QLDS), block
@@ -236,11 +237,11 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       }
     }
   };
-  // Lazy offsets at head_dim 256, tested lane-locally: a row's offset m only
-  // moves when some lane's max of its raw scores exceeds
+  // Lazy offsets with SB, tested lane-locally: a row's offset m only moves
+  // when some lane's max of its raw scores exceeds
   // thr = (m + kLazyLog2) / sl2; the cross-lane row max is only formed inside
-  // the (rare) rescale.  Head_dim 64 / 128 tests the row sums instead
-  // (commit) and forms lane maxima only when that test fires.
+  // the (rare) rescale.  Without SB the row sums are tested instead (commit)
+  // and lane maxima are formed only when that test fires.
   float thr[NT], rm[NT], tm[NT][4];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) thr[nt] = -INFINITY;
@@ -312,10 +313,10 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // The two phases of a step are woven by hand (one wave per SIMD issues in
   // order, so VALU work has to sit between the MFMAs of the instruction
   // stream); sched_barrier keeps the compiler from regrouping them.
-  // Head_dim 256 (SB):
+  // With SB:
   //   phase 1: S^T(u+1) (NM1 MFMAs) || softmax of S(u) (all 8 NT elements)
   //   phase 2: O^T += V^T P^T(u) (NM2 MFMAs) || the row-max test of S(u+1)
-  // Head_dim 64 / 128:
+  // Without SB:
   //   phase 1: S^T(u+1) || softmax elements [4 NT, 8 NT) of S(u)
   //   phase 2: O^T += V^T P^T(u) || softmax elements [0, 4 NT) of S(u+1)
   // with the lazy test after phase 1, on the row sums (commit).
@@ -390,7 +391,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
   };
-  // Phase 2 of head_dim 64 / 128: the P.V MFMAs row set by row set; once
+  // Phase 2 without SB: the P.V MFMAs row set by row set; once
   // row set nt' of P(u) has been read, row set nt' of P(u+1) is computed
   // (elements 8 nt' .. 8 nt' + 7 of S(u+1), over the next DT / 2 pairs).
   auto phase2s = [&](const SBuf& nx, const VSet& vf) {
@@ -410,7 +411,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // The lazy test of head_dim 64 / 128, after the softmax of half block st
+  // The lazy test without SB, after the softmax of half block st
   // is complete: a lane's sum of its eight P values above 2^kLazyLog2 means
   // the offset m of that row is stale (some P exceeded the lazy bound).
   // Then the offsets move to the half block's row maxima, l and O are
@@ -435,10 +436,11 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   KSet ka, kb;
   VSet va, vb;
   if constexpr (SB) {
-    // One K and one V^T set (head_dim 256: two would take 256 registers).
+    // One K and one V^T set (at head_dim 256 two would take 256 registers;
+    // at head_dim 128 the single set keeps fewer bytes in flight).
     // Step u: S(u) in cur, K(u+1) in ka, V(u) in va; K(u+2) is requested
-    // after phase 1 and V(u+1) after phase 2 — a phase ahead of use, which
-    // at this head_dim is about 2000 cycles.
+    // after phase 1 and V(u+1) after phase 2 — a phase ahead of use (about
+    // 2000 cycles at head_dim 256, 1000 at 128).
     auto step1 = [&](SBuf& cur, SBuf& nxt, int u) {
       const int rk = blk_raw(u + 2), rm1 = blk_raw(u + 1);
       phase1(cur, nxt, ka);
