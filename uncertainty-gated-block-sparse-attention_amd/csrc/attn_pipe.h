@@ -222,7 +222,21 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // or N, or not kept by every row).
   auto mask = [&](SBuf& st, int blk, int half, uint64_t mk) {
     const int kbase = blk * kBlock + 32 * half;
-    if ((kbase + 31 > row0) || (kbase + 32 > N) || mk != ~0ull) {
+    if (kbase + 31 <= row0 && kbase + 32 <= N) {
+      // causally visible and in bounds: only rows without the keep bit
+      // drop, each as a whole row set of S
+      if (mk != ~0ull) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const bool off = ((mk >> (rbase + 16 * nt + r16)) & 1ull) == 0;
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (off) st[mt][nt][i] = -INFINITY;
+        }
+      }
+    } else {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int row = row0 + 16 * nt + r16;
@@ -322,10 +336,9 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // with the lazy test after phase 1, on the row sums (commit).
   constexpr int NM1 = 2 * NT * KS, P1 = NM1 / 2;
   constexpr int E1ST = SB ? 0 : 4 * NT;             // first softmax element of phase 1
-  constexpr int EPP = (8 * NT - E1ST) / P1;         // softmax elements per MFMA pair
+  constexpr int NE1 = 8 * NT - E1ST;                // softmax elements of phase 1
   constexpr int NM2 = DT * NT, P2 = NM2 / 2;
   constexpr int RU = 4 * NT;                        // row-max units, spread over the P2 pairs
-  static_assert(EPP * P1 == 8 * NT - E1ST, "phase work must split evenly");
   auto phase1 = [&](const SBuf& cur, SBuf& nxt, const KSet& kf) {
     if constexpr (QLDS) {
       // pair j = (ks, nt): both M-tiles of fragment (nt, ks); the fragment
@@ -342,7 +355,8 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
           nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qr[j % 3],
                                      ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
 #pragma unroll
-        for (int e = E1ST + j * EPP; e < E1ST + (j + 1) * EPP; ++e) softmax_elem(cur, e);
+        for (int e = E1ST + (j * NE1 + P1 - 1) / P1; e < E1ST + ((j + 1) * NE1 + P1 - 1) / P1; ++e)
+          softmax_elem(cur, e);
         __builtin_amdgcn_sched_barrier(0);
       });
     } else {
@@ -354,7 +368,8 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
           nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
         }
 #pragma unroll
-        for (int e = E1ST + j * EPP; e < E1ST + (j + 1) * EPP; ++e) softmax_elem(cur, e);
+        for (int e = E1ST + (j * NE1 + P1 - 1) / P1; e < E1ST + ((j + 1) * NE1 + P1 - 1) / P1; ++e)
+          softmax_elem(cur, e);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
