@@ -28,12 +28,31 @@ PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
 
+# Selector policies of BASELINE configs[3]: the backbone (K-mean or Quest)
+# with and without the router; the budget comes from the config.
+POLICIES = {
+    "topk_mean": dict(mode="topk"),
+    "quest": dict(mode="quest"),
+    "router_mean": dict(mode="router", router_score="mean"),
+    "router_quest": dict(mode="router", router_score="quest"),
+}
+
+
+def policy_name(sel) -> str:
+    if sel.mode == "router":
+        return f"router-on-{sel.router_score}"
+    return "quest" if sel.mode == "quest" else f"{sel.mode} (K-mean)"
+
+
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="c2")
+    p.add_argument("--policy", choices=sorted(POLICIES), default=None,
+                   help="override the config's selector policy (configs[3] runs both "
+                        "backbones, K-mean and Quest, each with and without the router)")
     p.add_argument("--c3-layers", type=int, default=28,
                    help="stacked independent 128K layers for the configs[2] sweep (0 = skip)")
     p.add_argument("--no-dense", action="store_true")
@@ -369,7 +388,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the hot path shards by KV-head group; see DESIGN.md)", file=sys.stderr)
+              "(the hot path would shard by KV-head group; only the one-GPU share is built "
+              "and measured)", file=sys.stderr)
         sys.exit(2)
     import torch
     import synth
@@ -386,7 +406,10 @@ def main():
     if args.path == "v1":
         print(json.dumps(run_v1(args, cfg, q, k, v, torch)), flush=True)
         return
-    runner = LayerRunner(cfg, q, k, v)
+    fields = cfg.sel_fields()
+    if args.policy is not None:
+        fields.update(POLICIES[args.policy])
+    runner = LayerRunner(cfg, q, k, v, sel_fields=fields)
     ms_step, per = run_layer_bench(runner, args.steps, args.warmup, torch)
     attn_flops = runner.attended_flops()
     sel_bytes = runner.select_bytes()
@@ -407,7 +430,7 @@ def main():
         "data": "synthetic (seeded N(0,1) Q/K/V with planted needle blocks, synth.make_layer_fast on the GPU)",
         "config": {"workload": f"{cfg.name}: BASELINE configs[{cfg.index}] — one causal prefill "
                                f"attention layer, B={cfg.B} Hq={cfg.Hq} Hkv={cfg.Hkv} S={cfg.S} "
-                               f"D={cfg.D}, {cfg.mode}-on-{cfg.router_score} "
+                               f"D={cfg.D}, {policy_name(runner.sel)} "
                                f"k_base={runner.k_base} k_slots={runner.k_slots} "
                                f"q={cfg.router_quantile} {cfg.router_grain}-grain",
                    "seq_len": cfg.S, "global_batch": cfg.B},

@@ -38,15 +38,23 @@ __device__ uint32_t block_kth_smallest(F value_at, int64_t n, int64_t kth, uint3
       if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
     }
     __syncthreads();
-    if (tid == 0) {   // ascending scan for the bin holding the remaining-th smallest
-      uint32_t rem = *s_remaining, below = 0;
-      for (int d = 0; d < 256; ++d) {
-        if (below + hist[d] >= rem) {
-          *s_prefix = prefix | (static_cast<uint32_t>(d) << shift);
-          *s_remaining = rem - below;
-          break;
-        }
-        below += hist[d];
+    if (tid < 64) {
+      // ascending scan for the bin holding the remaining-th smallest: lane L
+      // owns bins 4L .. 4L + 3, a wavefront prefix sum over the lane totals
+      // finds the lane, the lane walks its four bins
+      const uint32_t rem = *s_remaining;
+      const uint32_t h0 = hist[4 * tid], h1 = hist[4 * tid + 1];
+      const uint32_t h2 = hist[4 * tid + 2], h3 = hist[4 * tid + 3];
+      const uint32_t below = wave_excl_scan(h0 + h1 + h2 + h3, tid);
+      const bool hit = below < rem && below + h0 + h1 + h2 + h3 >= rem;
+      if (hit) {   // exactly one lane: the counts are cumulative and rem <= total
+        uint32_t at = below;
+        int d = 4 * tid;
+        if (at + h0 < rem) { at += h0; ++d;
+          if (at + h1 < rem) { at += h1; ++d;
+            if (at + h2 < rem) { at += h2; ++d; } } }
+        *s_prefix = prefix | (static_cast<uint32_t>(d) << shift);
+        *s_remaining = rem - at;
       }
     }
     pmask |= 0xFFu << shift;
