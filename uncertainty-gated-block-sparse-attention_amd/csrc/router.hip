@@ -20,6 +20,23 @@
 
 namespace ugbsa {
 
+// Sum over h = 0 .. H-1 of x[h * stride], added in head order (the order of
+// ATen's CPU sum that the reference's mean runs), with the loads issued eight
+// at a time so that their latencies overlap.
+__device__ __forceinline__ float head_sum_in_order(const float* __restrict__ x, int H,
+                                                   int64_t stride) {
+  float acc = 0.f;
+  for (int h0 = 0; h0 < H; h0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = h0 + j < H ? x[(h0 + j) * stride] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (h0 + j < H) acc = h0 + j == 0 ? v[0] : acc + v[j];
+  }
+  return acc;
+}
+
 // k-th smallest (1-based) of value_at(0 .. n - 1) by one workgroup: a
 // 4-pass 8-bit radix select over the order-preserving float keys (NaN above
 // every number); returns the key to every thread.
@@ -76,8 +93,7 @@ __global__ __launch_bounds__(1024) void router_threshold_kernel(
   if (grain == kGrainRow) {
     for (int64_t i = tid; i < static_cast<int64_t>(B) * Qt; i += nt) {
       const int b = static_cast<int>(i / Qt), t = static_cast<int>(i % Qt);
-      float acc = sigma[(static_cast<int64_t>(b) * H) * Qt + t];
-      for (int h = 1; h < H; ++h) acc = acc + sigma[(static_cast<int64_t>(b) * H + h) * Qt + t];
+      const float acc = head_sum_in_order(sigma + (static_cast<int64_t>(b) * H) * Qt + t, H, Qt);
       const float mean = acc / static_cast<float>(H);
       for (int h = 0; h < H; ++h) sigma_eff[(static_cast<int64_t>(b) * H + h) * Qt + t] = mean;
     }
@@ -159,8 +175,7 @@ __global__ __launch_bounds__(1024) void router_rows_threshold_kernel(
   if (grain == kGrainRow) {
     for (int64_t i = tid; i < static_cast<int64_t>(B) * M; i += nt) {
       const int64_t b = i / M, row = i % M;
-      float acc = margin[(b * H) * M + row];
-      for (int h = 1; h < H; ++h) acc = acc + margin[(b * H + h) * M + row];
+      const float acc = head_sum_in_order(margin + (b * H) * M + row, H, M);
       const float mean = acc / static_cast<float>(H);
       for (int h = 0; h < H; ++h) margin_eff[(b * H + h) * M + row] = mean;
     }
