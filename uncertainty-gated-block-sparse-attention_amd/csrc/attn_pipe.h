@@ -78,6 +78,62 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   const int row0 = t * BM + rbase;
   const int q_last = t * BM + BM - 1;
 
+  // ---- Q tile requested first: its latency overlaps the list compaction ----
+  const uint16_t* qb = q + b * sq_b + h * sq_h;
+  // A negative scale is moved onto Q (bf16 negation is exact), so the
+  // scores the softmax sees are always scaled by sl2 > 0.
+  const float sl2 = fabsf(scale_log2);
+  const uint32_t qsign = scale_log2 < 0.f ? 0x80008000u : 0u;
+  u32x4 qraw[QLDS ? 1 : NT][QLDS ? 1 : KS];
+  if constexpr (!QLDS) {
+    // rows past M read row M - 1 (in bounds, no branch) and are zeroed below
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int row = min(row0 + 16 * nt + r16, M - 1);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qraw[nt][ks] = __builtin_bit_cast(u32x4, load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4));
+    }
+  }
+
+  // K and V^T operands of this KV head, in load order (kv_operand_kernel):
+  // half block (blk, half) = K slabs at ((2 blk + half) * 2 * KS) KiB and
+  // V^T slabs at ((2 blk + half) * DT) KiB; lane L reads 16 bytes at 16 L.
+  const int64_t head_elems = static_cast<int64_t>(NB) * kBlock * D;
+  const int64_t part = static_cast<int64_t>(B) * Hk * head_elems;
+  const uint16_t* kop_head = vt + (static_cast<int64_t>(b) * Hk + g) * head_elems;
+  const uint16_t* vop_head = kop_head + part;
+  typedef bf16x8 KSet[2][KS];
+  typedef bf16x8 VSet[DT];
+  auto uni = [](int x) -> int { return __builtin_amdgcn_readfirstlane(x); };
+  // Global (not buffer) loads: a wavefront streams K/V through the vector
+  // memory pipeline faster with them, and every visited block lies inside
+  // the operand copy, so no range check is needed.
+  auto load_k = [&](int blk, int half, KSet& kf) {
+    const uint16_t* p = kop_head + static_cast<int64_t>(2 * blk + half) * (2 * KS * 512) + lane * 8;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = load_bf16x8(p + (mt * KS + ks) * 512);
+  };
+  auto load_v = [&](int blk, int half, VSet& vf) {
+    const uint16_t* p = vop_head + static_cast<int64_t>(2 * blk + half) * (DT * 512) + lane * 8;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vf[dt] = load_bf16x8(p + dt * 512);
+  };
+  // The first operands are requested before the list is known, for block 0:
+  // the visited blocks are ascending and the selector forces the sink block
+  // 0 into every tile's list, so these loads overlap the list compaction.
+  // A list that starts elsewhere requests its first block again below.
+  // (Not with Q staged in LDS: at head_dim 256 it measured 1 % slower.)
+  KSet ka, kb;
+  VSet va, vb;
+  if constexpr (!QLDS) {
+    load_k(0, 0, ka);
+    if constexpr (!SB) load_k(0, 1, kb);
+    load_v(0, 0, va);
+  }
+
   // ---- visited blocks of this tile, compacted into LDS in ascending order ---
   // (the heads of a KV group and neighbouring tiles then sweep shared blocks
   // together, which keeps them in L2).  A block listed twice in a row keeps
@@ -96,18 +152,30 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   wave_lds_sync();
   int nv = 0;
   bool dup = false;
-  for (int base = 0; base < k_slots; base += 64) {
-    const int s = base + lane;
-    const int blk = s < k_slots ? idx[s] : -1;
-    const bool ok = blk >= 0 && blk < NB && blk * kBlock <= q_last;
-    const uint64_t bal = __ballot(ok);
-    if (ok) {
-      blist[nv + __popcll(bal & lt_mask)] = blk;
-      if (rmk != nullptr) mlist[nv + __popcll(bal & lt_mask)] = rmk[s];
-      const uint32_t bit = 1u << (blk & 31);
-      dup |= (atomicOr(&bits[blk >> 5], bit) & bit) != 0u;
+  // four slot groups of 64 per round, their loads issued together (one
+  // memory round trip per 256 slots instead of one per 64)
+  for (int base0 = 0; base0 < k_slots; base0 += 256) {
+    int blks[4];
+    uint64_t mks[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = base0 + 64 * j + lane;
+      blks[j] = s < k_slots ? idx[s] : -1;
+      mks[j] = rmk != nullptr && s < k_slots ? rmk[s] : 0ull;
     }
-    nv += __popcll(bal);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = blks[j];
+      const bool ok = blk >= 0 && blk < NB && blk * kBlock <= q_last;
+      const uint64_t bal = __ballot(ok);
+      if (ok) {
+        blist[nv + __popcll(bal & lt_mask)] = blk;
+        if (rmk != nullptr) mlist[nv + __popcll(bal & lt_mask)] = mks[j];
+        const uint32_t bit = 1u << (blk & 31);
+        dup |= (atomicOr(&bits[blk >> 5], bit) & bit) != 0u;
+      }
+      nv += __popcll(bal);
+    }
   }
   wave_lds_sync();
   // with row masks the slots are visited in their order (the masks are
@@ -130,32 +198,30 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   }
 
   // ---- Q tile: MFMA B operands held in registers ---------------------------
-  const uint16_t* qb = q + b * sq_b + h * sq_h;
   bf16x8 qf[QLDS ? 1 : NT][QLDS ? 1 : KS];
   // With QLDS the fragments are staged once in LDS in operand order —
   // fragment (nt, ks) is one KiB with lane L's 16 bytes at 16 L — and read
   // back one fragment per MFMA pair (ds_read_b128, conflict-free), which
   // keeps Q (4 KS VGPRs a row set) out of the register file.
   bf16x8* qs = reinterpret_cast<bf16x8*>(psm);
-  // A negative scale is moved onto Q (bf16 negation is exact), so the
-  // scores the softmax sees are always scaled by sl2 > 0.
-  const float sl2 = fabsf(scale_log2);
-  const uint32_t qsign = scale_log2 < 0.f ? 0x80008000u : 0u;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int row = row0 + 16 * nt + r16;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 x = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4,
-                                     load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
-                               : zero_bf16x8();
       if constexpr (QLDS) {
+        const bf16x8 x = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4,
+                                       load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
+                                 : zero_bf16x8();
         qs[(nt * KS + ks) * 64 + lane] = x;
       } else {
         // Q lives in AGPRs for the whole tile: the MFMAs read their B
         // operand from there, where a VGPR copy would be spilled to AGPRs
         // and copied back (v_accvgpr_read) for every use
-        u32x4 xa = __builtin_bit_cast(u32x4, x);
+        const uint32_t keep = row < M ? 0xFFFFFFFFu : 0u;
+        u32x4 xa = qraw[nt][ks];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xa[i] = (xa[i] ^ qsign) & keep;
         asm volatile("" : "+a"(xa));
         qf[nt][ks] = __builtin_bit_cast(bf16x8, xa);
       }
@@ -167,39 +233,13 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     else return qf[nt][ks];
   };
 
-  // K and V^T operands of this KV head, in load order (kv_operand_kernel):
-  // half block (blk, half) = K slabs at ((2 blk + half) * 2 * KS) KiB and
-  // V^T slabs at ((2 blk + half) * DT) KiB; lane L reads 16 bytes at 16 L.
-  const int64_t head_elems = static_cast<int64_t>(NB) * kBlock * D;
-  const int64_t part = static_cast<int64_t>(B) * Hk * head_elems;
-  const uint16_t* kop_head = vt + (static_cast<int64_t>(b) * Hk + g) * head_elems;
-  const uint16_t* vop_head = kop_head + part;
   const int nu = 2 * nv;
-
-  typedef bf16x8 KSet[2][KS];
-  typedef bf16x8 VSet[DT];
   typedef f32x4 SBuf[2][NT];
   // Half block u (clamped to the last one) -> its block id (LDS read; the
   // caller applies readfirstlane where it needs the id, so the read can be
   // issued early) and its half.
   auto clamp_u = [&](int u) -> int { return min(u, nu - 1); };
   auto blk_raw = [&](int u) -> int { return blist[clamp_u(u) >> 1]; };
-  auto uni = [](int x) -> int { return __builtin_amdgcn_readfirstlane(x); };
-  // Global (not buffer) loads: a wavefront streams K/V through the vector
-  // memory pipeline faster with them, and every visited block lies inside
-  // the operand copy, so no range check is needed.
-  auto load_k = [&](int blk, int half, KSet& kf) {
-    const uint16_t* p = kop_head + static_cast<int64_t>(2 * blk + half) * (2 * KS * 512) + lane * 8;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = load_bf16x8(p + (mt * KS + ks) * 512);
-  };
-  auto load_v = [&](int blk, int half, VSet& vf) {
-    const uint16_t* p = vop_head + static_cast<int64_t>(2 * blk + half) * (DT * 512) + lane * 8;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) vf[dt] = load_bf16x8(p + dt * 512);
-  };
 
   f32x4 o[DT][NT];
 #pragma unroll
@@ -448,8 +488,6 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   };
 
   SBuf sa, sb;
-  KSet ka, kb;
-  VSet va, vb;
   if constexpr (SB) {
     // One K and one V^T set (at head_dim 256 two would take 256 registers;
     // at head_dim 128 the single set keeps fewer bytes in flight).
@@ -472,8 +510,11 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       if (moved) rescale();
     };
     if (nv > 0) {
-      load_k(uni(blk_raw(0)), 0, ka);
-      load_v(uni(blk_raw(0)), 0, va);
+      const int b0 = uni(blk_raw(0));
+      if (QLDS || b0 != 0) {
+        load_k(b0, 0, ka);
+        load_v(b0, 0, va);
+      }
       qk(sa, ka);
       load_k(uni(blk_raw(1)), clamp_u(1) & 1, ka);
       mask(sa, uni(blk_raw(0)), 0, mbits(0));
@@ -513,9 +554,12 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     // the loads are issued in the loop's order (K(u+1), V(u), K(u+2),
     // V(u+1) outstanding at each step), so that the wait counts the compiler
     // derives for the loop hold for its first iteration as for the others
-    load_k(uni(blk_raw(0)), 0, ka);
-    load_k(uni(blk_raw(1)), 1, kb);
-    load_v(uni(blk_raw(0)), 0, va);
+    const int b0 = uni(blk_raw(0));
+    if (QLDS || b0 != 0) {
+      load_k(b0, 0, ka);
+      load_k(b0, 1, kb);
+      load_v(b0, 0, va);
+    }
     qk(sa, ka);
     load_k(uni(blk_raw(2)), clamp_u(2) & 1, ka);
     load_v(uni(blk_raw(1)), 1, vb);
