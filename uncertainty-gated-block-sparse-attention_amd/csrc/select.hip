@@ -145,6 +145,7 @@ __device__ inline uint32_t shrink_cand(uint64_t* cand, int n, int K, uint32_t* h
 // Top-K of trow[0 .. n_vis) by (score desc, block asc) into cand[0 ..
 // min(n_vis, K)) as composite keys (score key << 32 | ~block), unordered.
 // The wave's LDS row, histogram and candidate buffer; wave-local.
+template <int RK = kRegKeys>
 __device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int K, uint32_t* hist,
                                                uint64_t* cand, int lane, uint64_t lt_mask) {
   if (n_vis > K) {
@@ -154,16 +155,16 @@ __device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int
     uint32_t prefix = 0, pmask = 0;
     int remaining = K;
     bool fast = false;
-    if (n_vis <= 64 * kRegKeys) {
-      // Rows of up to 64 * kRegKeys blocks: keys in registers.  The digits
+    if (n_vis <= 64 * RK) {
+      // Rows of up to 64 * RK blocks: keys in registers.  The digits
       // start below the bits that every score except the two forced ones
       // shares (their AND / OR over the wavefront), so the first pass
       // spreads the scores over the bins instead of piling them into the
       // few that the exponent leaves.
       const int jmax = (n_vis + 63) / 64;
-      uint32_t key[kRegKeys];
+      uint32_t key[RK];
       uint32_t kand = 0xFFFFFFFFu, kor = 0u;
-      static_for<kRegKeys>([&](auto jc) {
+      static_for<RK>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         key[j] = 0u;
         if (j < jmax) {
@@ -183,7 +184,7 @@ __device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int
       // keys outside the common prefix (the forced ones, and any score that
       // does not share it): above or below the whole prefix range
       int above = 0, below = 0;
-      static_for<kRegKeys>([&](auto jc) {
+      static_for<RK>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         if (j < jmax) {
           const bool valid = lane + 64 * j < n_vis;
@@ -201,7 +202,7 @@ __device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int
           const uint32_t dmask = (1u << d) - 1u;
           for (int i = lane; i < 256; i += 64) hist[i] = 0;
           wave_lds_sync();
-          static_for<kRegKeys>([&](auto jc) {
+          static_for<RK>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             if (j < jmax && lane + 64 * j < n_vis && (key[j] & pmask) == prefix)
               atomicAdd(&hist[(key[j] >> shift) & dmask], 1u);
@@ -219,7 +220,7 @@ __device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int
         const int need_eq = remaining;
         const int n_gt = K - need_eq;
         int cnt_gt = 0, cnt_eq = 0;
-        static_for<kRegKeys>([&](auto jc) {
+        static_for<RK>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
           if (j < jmax) {
             const int i = lane + 64 * j;
@@ -643,7 +644,7 @@ __host__ __device__ constexpr int rows_wave_bytes(int NB, int KP) {
   return (NB * 4 + 15) / 16 * 16 + 256 * 4 + KP * 8;
 }
 
-template <int KP>
+template <int KP, int RK>
 __global__ __launch_bounds__(256) void select_rows_kernel(const RowsArgs a) {
   constexpr int R = KP / 64;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -669,7 +670,7 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const RowsArgs a) {
   wave_lds_sync();
 
   const int K = a.K;
-  select_to_cand(trow, n_vis, K, hist, cand, lane, lt_mask);
+  select_to_cand<RK>(trow, n_vis, K, hist, cand, lane, lt_mask);
   wave_lds_sync();
   const int n_sel = min(n_vis, K);
   uint64_t v[R];
@@ -735,11 +736,11 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const RowsArgs a) {
   }
 }
 
-template <int KP>
+template <int KP, int RK>
 static hipError_t launch_rows_t(const RowsArgs& a, hipStream_t stream) {
   const size_t lds = 4 * static_cast<size_t>(rows_wave_bytes(a.NB, KP));
   if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
-  auto kern = select_rows_kernel<KP>;
+  auto kern = select_rows_kernel<KP, RK>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds));
@@ -749,11 +750,21 @@ static hipError_t launch_rows_t(const RowsArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Keys held in registers per lane: the row's blocks / 64, so that short rows
+// keep fewer registers live and more wavefronts fit on a SIMD (this kernel
+// is latency-bound: one row per wavefront).
+template <int KP>
+static hipError_t launch_rows_k(const RowsArgs& a, hipStream_t stream) {
+  if (a.NB <= 64 * 8) return launch_rows_t<KP, 8>(a, stream);
+  if (a.NB <= 64 * 16) return launch_rows_t<KP, 16>(a, stream);
+  return launch_rows_t<KP, kRegKeys>(a, stream);
+}
+
 hipError_t launch_select_rows(const RowsArgs& a, hipStream_t stream) {
-  if (a.K <= 64) return launch_rows_t<64>(a, stream);
-  if (a.K <= 128) return launch_rows_t<128>(a, stream);
-  if (a.K <= 256) return launch_rows_t<256>(a, stream);
-  if (a.K <= 512) return launch_rows_t<512>(a, stream);
+  if (a.K <= 64) return launch_rows_k<64>(a, stream);
+  if (a.K <= 128) return launch_rows_k<128>(a, stream);
+  if (a.K <= 256) return launch_rows_k<256>(a, stream);
+  if (a.K <= 512) return launch_rows_k<512>(a, stream);
   return hipErrorInvalidValue;
 }
 
