@@ -39,20 +39,32 @@ __device__ __forceinline__ float head_sum_in_order(const float* __restrict__ x, 
 
 // k-th smallest (1-based) of value_at(0 .. n - 1) by one workgroup: a
 // 4-pass 8-bit radix select over the order-preserving float keys (NaN above
-// every number); returns the key to every thread.
+// every number); returns the key to every thread.  Each wavefront counts
+// into its own 256-bin histogram (hist holds kRouterWaves of them): the keys
+// of one pass mostly share their top digits, and one shared histogram would
+// serialise the LDS atomics of the whole workgroup on a few bins.
+constexpr int kRouterWaves = 16;   // 1024-thread workgroups
 template <class F>
 __device__ uint32_t block_kth_smallest(F value_at, int64_t n, int64_t kth, uint32_t* hist,
                                        uint32_t* s_prefix, uint32_t* s_remaining) {
   const int tid = threadIdx.x, nt = blockDim.x;
+  const int wave = tid >> 6;
+  uint32_t* whist = hist + wave * 256;
   if (tid == 0) { *s_prefix = 0; *s_remaining = static_cast<uint32_t>(kth); }
   uint32_t pmask = 0;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 256; i += nt) hist[i] = 0;
+    for (int i = tid; i < 256 * kRouterWaves; i += nt) hist[i] = 0;
     __syncthreads();
     const uint32_t prefix = *s_prefix;
     for (int64_t i = tid; i < n; i += nt) {
       const uint32_t key = float_key(value_at(i));
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      if ((key & pmask) == prefix) atomicAdd(&whist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 256) {   // fold the per-wave histograms into the first
+      uint32_t c = 0;
+      for (int w = 0; w < kRouterWaves; ++w) c += hist[w * 256 + tid];
+      hist[tid] = c;
     }
     __syncthreads();
     if (tid < 64) {
@@ -84,7 +96,7 @@ __global__ __launch_bounds__(1024) void router_threshold_kernel(
     const float* __restrict__ sigma, int B, int H, int Qt, int grain, int rmode, float tau,
     int64_t k_quant, float* __restrict__ sigma_eff, uint8_t* __restrict__ uncertain,
     float* __restrict__ threshold) {
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[256 * kRouterWaves];
   __shared__ uint32_t s_prefix, s_remaining;
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t n_all = static_cast<int64_t>(B) * H * Qt;
@@ -165,24 +177,31 @@ hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, in
 // int(q * n_elig)) from the host (0 when nothing is eligible); uncertain =
 // m_safe <= thr and eligible.  Abs: uncertain = margin < tau and eligible.
 // An uncertain cell keeps every visible block of its row.
-__global__ __launch_bounds__(1024) void router_rows_threshold_kernel(
-    const float* __restrict__ margin, int B, int H, int M, int grain, int rmode,
-    int64_t k_quant, int elig_row0, float* __restrict__ margin_eff, float* __restrict__ threshold) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t s_prefix, s_remaining;
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const int64_t n_all = static_cast<int64_t>(B) * H * M;
+// margin_eff: the head mean of each row for row grain (written for every
+// head), a copy of the margins for cell grain; one thread per (b, row) or
+// cell, over the whole grid.
+__global__ __launch_bounds__(256) void router_rows_mean_kernel(
+    const float* __restrict__ margin, int B, int H, int M, int grain,
+    float* __restrict__ margin_eff) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (grain == kGrainRow) {
-    for (int64_t i = tid; i < static_cast<int64_t>(B) * M; i += nt) {
-      const int64_t b = i / M, row = i % M;
-      const float acc = head_sum_in_order(margin + (b * H) * M + row, H, M);
-      const float mean = acc / static_cast<float>(H);
-      for (int h = 0; h < H; ++h) margin_eff[(b * H + h) * M + row] = mean;
-    }
+    if (i >= static_cast<int64_t>(B) * M) return;
+    const int64_t b = i / M, row = i % M;
+    const float mean = head_sum_in_order(margin + (b * H) * M + row, H, M) / static_cast<float>(H);
+    for (int h = 0; h < H; ++h) margin_eff[(b * H + h) * M + row] = mean;
   } else {
-    for (int64_t i = tid; i < n_all; i += nt) margin_eff[i] = margin[i];
+    if (i >= static_cast<int64_t>(B) * H * M) return;
+    margin_eff[i] = margin[i];
   }
-  __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void router_rows_threshold_kernel(
+    int B, int H, int M, int grain, int rmode, int64_t k_quant, int elig_row0,
+    const float* __restrict__ margin_eff, float* __restrict__ threshold) {
+  __shared__ uint32_t hist[256 * kRouterWaves];
+  __shared__ uint32_t s_prefix, s_remaining;
+  const int tid = threadIdx.x;
+  const int64_t n_all = static_cast<int64_t>(B) * H * M;
   if (rmode != kRouterQuantile || k_quant < 1) {
     if (tid == 0 && threshold != nullptr) *threshold = __uint_as_float(0x7FC00000u);
     return;
@@ -233,9 +252,15 @@ hipError_t launch_router_rows(const float* margin, int B, int H, int M, int NB, 
                               int rmode, float tau, int64_t k_quant, int elig_row0,
                               uint8_t* keep, float* margin_eff, uint8_t* uncertain,
                               float* threshold, hipStream_t stream) {
-  router_rows_threshold_kernel<<<1, 1024, 0, stream>>>(margin, B, H, M, grain, rmode, k_quant,
-                                                       elig_row0, margin_eff, threshold);
+  const int64_t n_mean = grain == kGrainRow ? static_cast<int64_t>(B) * M
+                                            : static_cast<int64_t>(B) * H * M;
+  router_rows_mean_kernel<<<dim3(static_cast<unsigned>((n_mean + 255) / 256)), 256, 0, stream>>>(
+      margin, B, H, M, grain, margin_eff);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  router_rows_threshold_kernel<<<1, 1024, 0, stream>>>(B, H, M, grain, rmode, k_quant, elig_row0,
+                                                       margin_eff, threshold);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = static_cast<int64_t>(B) * H * M;
   router_rows_fill_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), 256, 0, stream>>>(
