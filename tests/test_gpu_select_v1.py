@@ -170,7 +170,9 @@ def test_v1_select_vs_reference_golden(hip_lib, name):
 def test_v1_compute_kv_idx_and_rowmask(hip_lib):
     print("[case] v1 compute_kv_idx", flush=True)
     g = torch.Generator().manual_seed(3)
-    for (M, nb, bm) in ((1000, 16, 64), (512, 8, 32), (4096, 64, 64)):
+    # NB a multiple of 8 (8-byte row reads, one or two 512-block spans) and not
+    for (M, nb, bm) in ((1000, 16, 64), (512, 8, 32), (4096, 64, 64), (700, 11, 64),
+                        (640, 600, 64), (300, 1032, 32)):
         keep = torch.rand(2, 3, M, nb, generator=g) < 0.15
         keep[..., 0] = True
         kd = keep.to(DEV)
@@ -184,14 +186,13 @@ def test_v1_compute_kv_idx_and_rowmask(hip_lib):
         kp = np.zeros((2, 3, -(-M // bm) * bm, nb), bool)
         kp[:, :, :M] = keep.numpy()
         tiles = kp.reshape(2, 3, -1, bm, nb)
-        for b, h, t in ((0, 0, 0), (1, 2, -1), (0, 1, 3)):
-            for s in range(mk):
-                blk = kvf[b, h, t, s]
-                if blk == nb:
-                    assert rm[b, h, t, s] == 0
-                    continue
-                bits = sum(1 << r for r in range(bm) if tiles[b, h, t, r, blk])
-                assert int(rm[b, h, t, s]) == bits
+        # every listed block's row mask: bit r set where tile row r keeps it
+        weights = (np.uint64(1) << np.arange(bm, dtype=np.uint64))
+        want_rm = (tiles.transpose(0, 1, 2, 4, 3).astype(np.uint64) * weights).sum(-1)
+        blk = np.minimum(kvf, nb - 1)
+        got = np.take_along_axis(want_rm, blk.astype(np.int64), axis=-1)
+        got[kvf == nb] = 0
+        assert np.array_equal(rm, got.astype(np.uint64))
 
 
 @pytest.mark.parametrize("D,Hq,Hk,bm", [(64, 4, 2, 64), (128, 4, 1, 64), (256, 2, 1, 64),

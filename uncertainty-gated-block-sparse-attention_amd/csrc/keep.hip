@@ -9,9 +9,13 @@
 // — the per-row keep test of the reference kernel (:87-103), read by the
 // attention kernels once per block instead of once per row.
 //
-// One wavefront per tile, 64 blocks at a time (a block per lane): the lane
-// ORs its block's keep bytes over the tile's rows (each row's 64 bytes are
-// one coalesced read) and a ballot compacts the kept blocks in order.
+// One wavefront per tile.  When rows are a multiple of 8 bytes (NB % 8 == 0,
+// mask 8-byte aligned)
+// a lane owns 8 consecutive blocks of each 512-block span and reads them as
+// one 8-byte word per row (a row's span is one coalesced 512-byte read), ORs
+// the row bits into 8 masks, and a wavefront prefix sum over the lanes'
+// counts places the kept blocks in ascending order.  Otherwise 64 blocks at
+// a time, one block per lane, with a ballot compaction.
 #include "common.h"
 #include "launch.h"
 
@@ -31,6 +35,39 @@ __global__ __launch_bounds__(256) void keep_kv_idx_kernel(
   uint64_t* rm = rowmask != nullptr ? rowmask + unit * NB : nullptr;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int cnt = 0;
+  if ((NB & 7) == 0 && (reinterpret_cast<uintptr_t>(keep) & 7) == 0) {
+    for (int base = 0; base < NB; base += 512) {
+      const int b0 = base + 8 * lane;
+      uint64_t mk[8] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
+      if (b0 < NB) {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(kb + b0);
+        const int64_t stride = NB / 8;
+        for (int r0 = 0; r0 < rows; r0 += 8) {
+          uint64_t w[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) w[j] = r0 + j < rows ? src[(r0 + j) * stride] : 0ull;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              mk[i] |= static_cast<uint64_t>(((w[j] >> (8 * i)) & 0xFFull) != 0) << (r0 + j);
+        }
+      }
+      int mine = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mine += mk[i] != 0ull;
+      int pos = cnt + static_cast<int>(wave_excl_scan(static_cast<uint32_t>(mine), lane));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (mk[i] != 0ull) {
+          out[pos] = b0 + i;
+          if (rm != nullptr) rm[pos] = mk[i];
+          ++pos;
+        }
+      }
+      cnt = __shfl(pos, 63, 64);
+    }
+  } else {
   for (int base = 0; base < NB; base += 64) {
     const int blk = base + lane;
     uint64_t mask = 0;
@@ -45,6 +82,7 @@ __global__ __launch_bounds__(256) void keep_kv_idx_kernel(
       if (rm != nullptr) rm[pos] = mask;
     }
     cnt += __popcll(bal);
+  }
   }
   for (int s = cnt + lane; s < NB; s += 64) {
     out[s] = NB;
