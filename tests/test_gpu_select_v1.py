@@ -96,7 +96,8 @@ def check_on_kernel_scores(res, sel, N, history=None):
 @pytest.mark.parametrize("policy", sorted(POLICIES))
 def test_v1_select_exact_on_kernel_scores(hip_lib, D, policy):
     print(f"[case] v1 select D={D} policy={policy}", flush=True)
-    S = 2000 if D != 128 else 4096                         # ragged and aligned
+    # ragged (NB 32), aligned (NB 64), and NB 21 (keep rows not a multiple of 8 bytes)
+    S = {64: 2000, 128: 4096, 256: 1300}[D]
     q, k, _ = synth.make_layer(synth.CONFIGS["c1"], 7, S=S, D=D, dtype=torch.bfloat16)
     sel = make_sel(budget_blocks=5, k_min=2, k_max=12, **POLICIES[policy])
     qd, kd = q.to(DEV), k.to(DEV)

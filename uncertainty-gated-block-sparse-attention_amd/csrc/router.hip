@@ -244,7 +244,16 @@ __global__ __launch_bounds__(256) void router_rows_fill_kernel(
   if (unc) {
     uint8_t* kr = keep + i * NB;
     const int last = row / kBlock;
-    for (int blk = lane; blk < NB; blk += 64) kr[blk] = blk <= last ? 1 : 0;
+    if ((NB & 7) == 0 && (reinterpret_cast<uintptr_t>(keep) & 7) == 0) {
+      for (int b0 = 8 * lane; b0 < NB; b0 += 512) {   // eight flags per 8-byte store
+        uint64_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w |= static_cast<uint64_t>(b0 + j <= last) << (8 * j);
+        *reinterpret_cast<uint64_t*>(kr + b0) = w;
+      }
+    } else {
+      for (int blk = lane; blk < NB; blk += 64) kr[blk] = blk <= last ? 1 : 0;
+    }
   }
 }
 

@@ -722,7 +722,17 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const RowsArgs a) {
   }
   wave_lds_sync();
   uint8_t* kr = a.keep + (bh * a.M + row) * NB;
-  for (int blk = lane; blk < NB; blk += 64) kr[blk] = static_cast<uint8_t>(flag[blk]);
+  if ((NB & 7) == 0 && (reinterpret_cast<uintptr_t>(a.keep) & 7) == 0) {
+    // eight flags per lane packed into one 8-byte store
+    for (int b0 = 8 * lane; b0 < NB; b0 += 512) {
+      uint64_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w |= static_cast<uint64_t>(flag[b0 + i] & 1u) << (8 * i);
+      *reinterpret_cast<uint64_t*>(kr + b0) = w;
+    }
+  } else {
+    for (int blk = lane; blk < NB; blk += 64) kr[blk] = static_cast<uint8_t>(flag[blk]);
+  }
 
   if (a.margin != nullptr) {
     // (s[k_eff - 1] - s[k_eff]) / max(s[0] - s[k_eff], 1e-6); NaN kept
