@@ -223,32 +223,44 @@ __global__ __launch_bounds__(1024) void router_rows_threshold_kernel(
   if (tid == 0 && threshold != nullptr) *threshold = thr;
 }
 
+// Trigger decisions for 64 consecutive (b, h, row) cells per wavefront, one
+// cell per lane (coalesced flag writes); then the wavefront writes the keep
+// row of each triggered cell in turn: its visible blocks 0 .. row / 64.
 __global__ __launch_bounds__(256) void router_rows_fill_kernel(
     const float* __restrict__ margin_eff, const float* __restrict__ threshold, int B, int H,
     int M, int NB, int rmode, float tau, int64_t k_quant, int elig_row0,
     uint8_t* __restrict__ uncertain, uint8_t* __restrict__ keep) {
   const int lane = threadIdx.x & 63;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (i >= static_cast<int64_t>(B) * H * M) return;
-  const int row = static_cast<int>(i % M);
-  const bool elig = row >= elig_row0;
-  const float e = margin_eff[i];
-  bool unc;
-  if (rmode == kRouterQuantile) {
-    const float ms = e == e ? e : INFINITY;
-    unc = k_quant > 0 && elig && ms <= *threshold;
-  } else {
-    unc = elig && e < tau;
+  const int64_t n = static_cast<int64_t>(B) * H * M;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64;
+  if (c0 >= n) return;
+  const int64_t i = c0 + lane;
+  bool unc = false;
+  if (i < n) {
+    const int row = static_cast<int>(i % M);
+    const bool elig = row >= elig_row0;
+    const float e = margin_eff[i];
+    if (rmode == kRouterQuantile) {
+      const float ms = e == e ? e : INFINITY;
+      unc = k_quant > 0 && elig && ms <= *threshold;
+    } else {
+      unc = elig && e < tau;
+    }
+    uncertain[i] = unc ? 1 : 0;
   }
-  if (lane == 0) uncertain[i] = unc ? 1 : 0;
-  if (unc) {
-    uint8_t* kr = keep + i * NB;
-    const int last = row / kBlock;
-    if ((NB & 7) == 0 && (reinterpret_cast<uintptr_t>(keep) & 7) == 0) {
+  const bool wide = (NB & 7) == 0 && (reinterpret_cast<uintptr_t>(keep) & 7) == 0;
+  uint64_t pending = __ballot(unc);
+  while (pending) {
+    const int j = __ffsll(static_cast<long long>(pending)) - 1;
+    pending &= pending - 1;
+    const int64_t cell = c0 + j;
+    uint8_t* kr = keep + cell * NB;
+    const int last = static_cast<int>(cell % M) / kBlock;
+    if (wide) {
       for (int b0 = 8 * lane; b0 < NB; b0 += 512) {   // eight flags per 8-byte store
         uint64_t w = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) w |= static_cast<uint64_t>(b0 + j <= last) << (8 * j);
+        for (int q = 0; q < 8; ++q) w |= static_cast<uint64_t>(b0 + q <= last) << (8 * q);
         *reinterpret_cast<uint64_t*>(kr + b0) = w;
       }
     } else {
@@ -272,7 +284,8 @@ hipError_t launch_router_rows(const float* margin, int B, int H, int M, int NB, 
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = static_cast<int64_t>(B) * H * M;
-  router_rows_fill_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), 256, 0, stream>>>(
+  const int64_t waves = (rows + 63) / 64;
+  router_rows_fill_kernel<<<dim3(static_cast<unsigned>((waves + 3) / 4)), 256, 0, stream>>>(
       margin_eff, threshold, B, H, M, NB, rmode, tau, k_quant, elig_row0, uncertain, keep);
   return hipGetLastError();
 }
