@@ -143,13 +143,21 @@ class LayerRunner:
                                  kv_idx.shape[2], kv_idx.shape[3], 64, float(self.cfg.scaling),
                                  o.data_ptr(), *o.stride(), self.ws.data_ptr(), s), "attention")
 
-    def attended_flops(self, kv_idx=None) -> float:
-        """Executed attention FLOPs: 4 * 64 * 64 * D per visited (tile, block)."""
+    def attended_flops(self, kv_idx=None, exact=False) -> float:
+        """Attention FLOPs over the visited (tile, block) pairs of kv_idx.
+        Executed (default): 4 * 64 * 64 * D per visit, the diagonal block in
+        full, as the kernel computes it.  exact: only the (row, key) pairs the
+        causal mask keeps, 4 * D each — 64 * 65 / 2 = 2080 pairs on the
+        diagonal block (the layer shapes are whole blocks)."""
         torch = self.torch
         kv = self.kv_idx if kv_idx is None else kv_idx
         t = torch.arange(kv.shape[2], device=kv.device).view(1, 1, -1, 1)
         ok = (kv >= 0) & (kv < self.NB) & (kv <= t)
-        return float(ok.sum().item()) * 4.0 * 64 * 64 * self.D
+        visits = float(ok.sum().item())
+        if not exact:
+            return visits * 4.0 * 64 * 64 * self.D
+        diag = float((ok & (kv == t)).sum().item())
+        return ((visits - diag) * 64 * 64 + diag * 64 * 65 / 2) * 4.0 * self.D
 
     def select_bytes(self) -> dict:
         """Algorithmic HBM bytes of kernels 1 and 2 (one launch each)."""
@@ -244,11 +252,22 @@ def dense_kernel3_ms(runner, torch, steps=3):
     return ms, flops
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
-    """The CPU oracle (numpy fp32) timed on a bounded sample of the same layer:
-    the full selector for one KV group (its query heads) and masked dense
-    attention (reference_attn cost) over every tile of whole heads until the
-    time budget is spent; both scaled to one full layer."""
+    """The CPU oracle (numpy fp32) on the same layer: the v2 selector over
+    every KV group and masked dense attention (reference_attn cost) over every
+    head, timed in full when the config is BASELINE configs[0] or [1] (about
+    35 s at configs[1]); longer layers stop after budget_s of attention and
+    scale by the heads done."""
     from threadpoolctl import threadpool_info
     sys.path.insert(0, ROOT)
     from oracle import attention as OA
@@ -256,59 +275,96 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
     import sparse_attention as sa
 
     grp = cfg.Hq // cfg.Hkv
-    qs = q[:, :grp].float().cpu().numpy()
-    ks = k[:, :1].float().cpu().numpy()
+    full = cfg.index <= 1
     sel = sa.Selector()
     for f, val in cfg.sel_fields().items():
         setattr(sel, f, val)
     ocfg = OS.SelectorConfig.from_selector(sel)
+    qn = q.float().cpu().numpy()
+    kn = k.float().cpu().numpy()
+    vn = v.float().cpu().numpy()
     t0 = time.perf_counter()
-    OS.select_kv_idx_v2(qs, ks, cfg.scaling, ocfg)
-    sel_s = (time.perf_counter() - t0) * cfg.Hkv
-    # masked dense attention (reference_attn cost): whole heads, in order, until the budget
+    if full:
+        OS.select_kv_idx_v2(qn, kn, cfg.scaling, ocfg)
+        sel_s = time.perf_counter() - t0
+    else:
+        OS.select_kv_idx_v2(qn[:, :grp], kn[:, :1], cfg.scaling, ocfg)
+        sel_s = (time.perf_counter() - t0) * cfg.Hkv
     qt = kv_idx.shape[2]
     kv_np = kv_idx.cpu().numpy()
     t0 = time.perf_counter()
     heads_done = 0
     for h in range(cfg.Hq):
         kh = h // grp
-        OA.masked_tile_attention(q[:, h:h + 1].float().cpu().numpy(),
-                                 k[:, kh:kh + 1].float().cpu().numpy(),
-                                 v[:, kh:kh + 1].float().cpu().numpy(),
+        OA.masked_tile_attention(qn[:, h:h + 1], kn[:, kh:kh + 1], vn[:, kh:kh + 1],
                                  kv_np[:, h:h + 1], cfg.scaling)
         heads_done += 1
-        if time.perf_counter() - t0 > budget_s:
+        if not full and time.perf_counter() - t0 > budget_s:
             break
     att_sample_s = time.perf_counter() - t0
     att_s = att_sample_s / heads_done * cfg.Hq
     threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    if full:
+        sample = (f"numpy fp32 oracle on the whole {cfg.name} layer: v2 selector over all "
+                  f"{cfg.Hkv} KV groups ({sel_s:.1f} s) and masked dense attention "
+                  f"(reference_attn cost, all {qt} tiles of all {cfg.Hq} heads, {att_s:.1f} s); "
+                  f"CPU: {cpu_model()}")
+    else:
+        sample = (f"numpy fp32 oracle on {cfg.name}: v2 selector for 1 of {cfg.Hkv} KV groups "
+                  f"({sel_s / cfg.Hkv:.1f} s, x{cfg.Hkv}); masked dense attention (reference_attn "
+                  f"cost, all {qt} tiles) for {heads_done} of {cfg.Hq} heads "
+                  f"({att_sample_s:.1f} s, x{cfg.Hq / heads_done:.2f}); CPU: {cpu_model()}")
     return {
         "value": round((sel_s + att_s) * 1e3, 1),
         "unit": "ms/layer",
         "cores": int(threads),
         "kind": "port",
-        "sample": (f"numpy fp32 oracle on {cfg.name}: full v2 selector for 1 of {cfg.Hkv} KV groups "
-                   f"({sel_s / cfg.Hkv:.1f} s, x{cfg.Hkv}); masked dense attention (reference_attn "
-                   f"cost, all {qt} tiles) for {heads_done} of {cfg.Hq} heads "
-                   f"({att_sample_s:.1f} s, x{cfg.Hq / heads_done:.2f})"),
+        "sample": sample,
+        "cpu_model": cpu_model(),
         "select_ms": round(sel_s * 1e3, 1),
         "attention_ms": round(att_s * 1e3, 1),
     }
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "attn_fwd_c2_traffic.md")
+def traffic_profile(cfg_name):
+    """The committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of a workload."""
+    return os.path.join("profiles", f"attn_fwd_{cfg_name}_traffic.md")
 
 
 def measured_traffic(cfg_name):
-    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary of this workload (calibrated against a 1 GiB copy)."""
+    """HBM bytes per attention launch (all launches of one layer) from the
+    committed FETCH_SIZE / WRITE_SIZE summary of this workload, calibrated
+    against a 1 GiB copy; None if the workload has no summary."""
     try:
-        for line in open(TRAFFIC_PROFILE):
+        for line in open(os.path.join(ROOT, traffic_profile(cfg_name))):
             if line.startswith(f"traffic_bytes attn_fwd_pipe_kernel {cfg_name}:"):
                 return float(line.split(":")[1])
     except OSError:
         pass
     return None
+
+
+def attention_kernel_label(D, NB):
+    """The attn_fwd_pipe_kernel<D, NT, QLDS, SB> instance launch_attn_fwd
+    runs for 64-row tiles (csrc/attn_fwd.hip)."""
+    if D == 256:
+        return "attn_fwd_pipe_kernel<256, 2, true, true>"
+    return f"attn_fwd_pipe_kernel<{D}, 4, false, {'true' if D == 128 and NB > 1024 else 'false'}>"
+
+
+def roofline(cfg_name, D, NB, tflops):
+    return {
+        "bound": "mfma",
+        "kernel": attention_kernel_label(D, NB),
+        "achieved": round(tflops, 1),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "traffic": measured_traffic(cfg_name),
+        "traffic_source": (traffic_profile(cfg_name) + " (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                           "calibrated by a 1 GiB copy)"
+                           if measured_traffic(cfg_name) is not None else None),
+    }
 
 
 def pmc_run(cfg, steps, torch, synth, dev):
@@ -412,6 +468,7 @@ def main():
     runner = LayerRunner(cfg, q, k, v, sel_fields=fields)
     ms_step, per = run_layer_bench(runner, args.steps, args.warmup, torch)
     attn_flops = runner.attended_flops()
+    exact_flops = runner.attended_flops(exact=True)
     sel_bytes = runner.select_bytes()
     attn_tflops = attn_flops / (per["attention"] * 1e-3) / 1e12
     select_ms = per["summary"] + per["select"] + per["router"]
@@ -438,6 +495,8 @@ def main():
         "select_ms": round(select_ms, 4),
         "attended_tflop": round(attn_flops / 1e12, 4),
         "attended_tflops": round(attn_tflops, 1),
+        "causal_exact_tflop": round(exact_flops / 1e12, 4),
+        "causal_exact_tflops": round(exact_flops / (per["attention"] * 1e-3) / 1e12, 1),
         "trigger_rate": round(float(runner.unc.float().mean().item()), 4) if runner.router else None,
         "hbm_gbs": {
             "summary": round(sel_bytes["summary"] / (per["summary"] * 1e-3) / 1e9, 1),
@@ -445,18 +504,7 @@ def main():
         },
         "select_mfma_frac": round(runner.select_flops() / (per["select"] * 1e-3) / 1e12
                                   / PEAK_BF16_TFLOPS, 4),
-        "roofline": {
-            "bound": "mfma",
-            "kernel": (f"attn_fwd_pipe_kernel<{cfg.D}>" if cfg.D in (64, 128)
-                       else f"attn_fwd_kernel<{cfg.D}>"),
-            "achieved": round(attn_tflops, 1),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic(cfg.name),
-            "traffic_source": "profiles/attn_fwd_c2_traffic.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
-                              "calibrated by a 1 GiB copy)",
-        },
+        "roofline": roofline(cfg.name, cfg.D, runner.NB, attn_tflops),
         "gen_s": round(gen_s, 1),
     }
     if not args.no_dense:
@@ -485,12 +533,16 @@ def main():
         r0 = layers[0]
         ms1, per3 = run_layer_bench(r0, max(3, args.steps // 2), 1, torch)
         fl3 = r0.attended_flops()
+        ex3 = r0.attended_flops(exact=True)
         tf3 = fl3 / (per3["attention"] * 1e-3) / 1e12
         c3res = {"layers": args.c3_layers, "ms_per_layer": round(ms_sweep / args.c3_layers, 3),
                  "single_layer_ms": round(ms1, 3),
                  "kernels_ms": {k_: round(v_, 3) for k_, v_ in per3.items()},
                  "attended_tflop": round(fl3 / 1e12, 3), "attended_tflops": round(tf3, 1),
-                 "mfma_frac": round(tf3 / PEAK_BF16_TFLOPS, 4)}
+                 "causal_exact_tflop": round(ex3 / 1e12, 3),
+                 "causal_exact_tflops": round(ex3 / (per3["attention"] * 1e-3) / 1e12, 1),
+                 "mfma_frac": round(tf3 / PEAK_BF16_TFLOPS, 4),
+                 "roofline": roofline("c3", c3.D, r0.NB, tf3)}
         if not args.no_dense:
             sd3, _ = dense_sdpa_ms(r0.q, r0.k, r0.v, c3.scaling, torch, steps=2)
             k33, k3f = dense_kernel3_ms(r0, torch, steps=2)

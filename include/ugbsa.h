@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define UGBSA_ABI_VERSION 1
+#define UGBSA_ABI_VERSION 2
 
 #define UGBSA_OK 0
 #define UGBSA_EARG (-1)     /* bad size / value / null pointer */

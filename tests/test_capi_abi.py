@@ -40,7 +40,10 @@ def test_size_queries(lib):
     # [B, Hk, NB, P, D]: c3 Quest = 1 * 4 * 2048 * 2 * 128
     assert lib.ugbsa_summary_elems(1, 4, 131072, 128, _capi.MODE_QUEST) == 4 * 2048 * 2 * 128
     assert lib.ugbsa_summary_elems(1, 2, 1000, 64, _capi.MODE_MEAN) == 2 * 16 * 3 * 64
-    assert lib.ugbsa_attn_workspace_elems(1, 4, 1000, 128) == 2 * 4 * 16 * 64 * 128
+    # K and V operand copies, then the tile schedule (2 * B * NB int32 = 4 * B * NB bf16,
+    # rounded to 16 bytes)
+    assert lib.ugbsa_attn_workspace_elems(1, 4, 1000, 128) == 2 * 4 * 16 * 64 * 128 + 64
+    assert lib.ugbsa_attn_workspace_elems(2, 2, 131072, 256) == 2 * 2 * 2 * 2048 * 64 * 256 + 4 * 2 * 2048
 
 
 def test_argument_errors_are_reported_without_launch(lib):
@@ -67,6 +70,14 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"k_quant" in lib.ugbsa_last_error()
     with pytest.raises(AssertionError):
         _capi.check(rc, "router")
+    # one-shot prefill: query length must equal key length
+    rc = lib.ugbsa_select(16, 0, 0, 8, 1, 16, 1, 8, 2, 64, 128, 128, _capi.DTYPE_BF16,
+                          _capi.MODE_QUEST, 0.1, 1, 1, 64, 16, None, None, None)
+    assert rc == -1 and b"query length" in lib.ugbsa_last_error()
+    rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
+                            1, 8, 2, 64, 128, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
+                            16, 0, 0, 8, 1, 16, None)
+    assert rc == -1 and b"query length" in lib.ugbsa_last_error()
     # score dump: rho_k must stay below NB (the reference indexes s(rho_k))
     rc = lib.ugbsa_score_dump(16, 0, 0, 8, 1, 16, 1, 8, 2, 256, 256, 128, _capi.DTYPE_BF16,
                               _capi.MODE_QUEST, 0.1, 2, 4, 16, 16, 16, 16, 16, 16, None, None)

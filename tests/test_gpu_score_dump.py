@@ -182,7 +182,7 @@ def test_dump_hook_through_hf_model(hip_lib, tmp_path):
             assert s["tau_hat"].shape == (1, 4) and (s["tau_hat"] > 0).all()
             assert (s["sigma"][..., s["valid"]] <= 1).all()
     finally:
-        if dbs._STATE["enabled"]:
+        if dbs._session is not None:
             dbs.flush_and_teardown()
         sa.SEL.__dict__.update(saved)
         sa.SEL.reset_log()

@@ -9,7 +9,8 @@ Bars:
 * kernel row scores vs oracle scores from the same bf16 inputs — |dS| <=
   1e-5 * max(1, |S|) (fp32 sums of up to 2 * 256 products, in other orders);
 * keep vs the reference's own masks (golden vectors): differing blocks only
-  at the row's cut score (ties, and near ties within 2e-6 of it);
+  at the row's cut score (ties, and near ties within twice the row's measured
+  kernel-vs-reference score gap, at least 1e-6);
 * _compute_kv_idx / row masks exact; attention over a keep mask within
   max-abs 2e-2 / mean-abs 2e-3 of the fp32 oracle (head_dim 64/128/256,
   GQA, 64- and 32-row tiles, through the HF dispatcher).
@@ -24,6 +25,7 @@ import synth
 from block_attn import _compute_kv_idx, block_sparse_attn, keep_kv_idx
 from oracle import attention as OA
 from oracle import selector_v1 as V1
+from parity import score_gap_tol
 from test_oracle_selector_v1 import CASES, load_v1, ranked, unpack_keep
 
 pytestmark = pytest.mark.gpu
@@ -162,10 +164,56 @@ def test_v1_select_vs_reference_golden(hip_lib, name):
             if bad_rows.any():
                 srt = -np.sort(-ref_sc, axis=-1)
                 cut = np.take_along_axis(srt, np.minimum(counts, nb)[..., None] - 1, axis=-1)[..., 0]
-                near = np.abs(ref_sc - cut[..., None]) <= 2e-6
+                # within twice the row's measured score gap (at least the
+                # contract's 1e-6 tie window) of the cut
+                tol = score_gap_tol(ref_sc, res.scores.cpu().numpy()).reshape(ref_sc.shape[:-1])
+                with np.errstate(invalid="ignore"):
+                    near = np.abs(ref_sc - cut[..., None]) <= tol[..., None]
                 near |= np.isinf(ref_sc) & np.isinf(cut[..., None])
                 assert not (diff & ~near).any(), f"{pol}/L{layer}: blocks differ off the cut"
             print(f"  {pol}/L{layer}: {int(bad_rows.sum())} rows differ at cut ties", flush=True)
+
+
+@pytest.mark.parametrize("policy", ["topk", "belief", "rollout", "router_quest_row_q",
+                                    "router_mean_cell_q"])
+@pytest.mark.parametrize("tiles_per_pass", [1, 3])
+def test_v1_multipass_equals_single_pass(hip_lib, monkeypatch, policy, tiles_per_pass):
+    """Above its workspace bound the per-row selector scores rows in passes of
+    whole 64-row tiles (ugbsa_select_mask: rows_t0 / rows_t1 offsets into the
+    row-score buffer).  Forced down to 1 or 3 tiles per pass, with a ragged
+    last tile, every output equals the single-pass run bit for bit."""
+    print(f"[case] v1 multipass {policy} x{tiles_per_pass}", flush=True)
+    cfg = synth.CONFIGS["c1"]
+    S, D = 64 * 9 + 23, 128
+    q, k, _ = synth.make_layer(cfg, 5, S=S, dtype=torch.bfloat16)
+    qd, kd = q.to(DEV), k.to(DEV)
+    B, H, nb = q.shape[0], q.shape[1], (S + 63) // 64
+    fields = dict(budget_blocks=3, k_min=1, **POLICIES[policy])
+
+    def run(ws_elems):
+        sel = make_sel(**fields)
+        res = []
+        for _ in range(2 if policy == "rollout" else 1):   # the history feeds the next call
+            if ws_elems is None:
+                r = sa.select_mask_v1(qd, kd, D ** -0.5, sel=sel, want_scores=True)
+            else:
+                monkeypatch.setattr(sa, "_V1_WORKSPACE_ELEMS", ws_elems)
+                r = sa.select_mask_v1(qd, kd, D ** -0.5, sel=sel)
+            torch.cuda.synchronize()
+            res.append(r)
+        return res, sel
+
+    one, sel1 = run(None)
+    many, seln = run(B * H * 64 * nb * tiles_per_pass)
+    for a, b in zip(one, many):
+        assert torch.equal(a.keep, b.keep)
+        for f in ("margin", "margin_eff", "uncertain", "threshold"):
+            x, y = getattr(a, f), getattr(b, f)
+            assert (x is None) == (y is None), f
+            if x is not None:
+                assert same_bits(x.cpu().numpy(), y.cpu().numpy()), f
+    if policy == "rollout":
+        assert same_bits(sel1.selection_history.cpu().numpy(), seln.selection_history.cpu().numpy())
 
 
 def test_v1_compute_kv_idx_and_rowmask(hip_lib):

@@ -52,40 +52,9 @@ def test_sparse_modes_need_the_hip_library_on_cpu():
         sa.SEL.mode, sa.SEL.kernel_v2 = saved
 
 
-def test_install_rollout_hooks_captures_prefill_inputs():
-    """src/sparse_attention.py:188-205: every decoder layer's prefill input is
-    kept in SEL.hidden_at (decode steps are not), and SEL.model_ref is set."""
-    from transformers import AutoModelForCausalLM
-    from transformers.models.qwen2 import Qwen2Config
-    cfg = Qwen2Config(vocab_size=64, hidden_size=64, intermediate_size=96,
-                      num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=2,
-                      max_position_embeddings=512)
-    saved = dict(sa.SEL.__dict__)
-    try:
-        sa.SEL.mode = "dense"
-        torch.manual_seed(0)
-        model = AutoModelForCausalLM.from_config(cfg, attn_implementation="block_sparse").eval()
-        sa.install_rollout_hooks(model)
-        assert sa.SEL.model_ref is model and sa.SEL.hidden_at == {}
-        ids = torch.randint(0, 64, (1, 40), generator=torch.Generator().manual_seed(1))
-        with torch.no_grad():
-            model(ids)
-        assert sorted(sa.SEL.hidden_at) == [0, 1, 2]
-        assert all(h.shape == (1, 40, 64) for h in sa.SEL.hidden_at.values())
-        first = sa.SEL.hidden_at[0].clone()
-        with torch.no_grad():
-            emb = model.model.embed_tokens(ids)
-        assert torch.equal(first, emb)                 # layer 0's input is the embedding
-        with torch.no_grad():
-            model(ids[:, :1])                          # a one-token step is not kept
-        assert torch.equal(sa.SEL.hidden_at[0], first)
-    finally:
-        sa.SEL.__dict__.clear()
-        sa.SEL.__dict__.update(saved)
-
-
-def test_rollout_peek_needs_the_hip_library_on_cpu():
-    """rollout_peek takes its baseline from the HIP v1 selector: no CPU path."""
+def test_rollout_peek_is_out_of_scope():
+    """rollout_peek (an abandoned research mode of the reference, off its v2
+    path) raises instead of running."""
     q = torch.zeros(1, 4, 128, 64, dtype=torch.bfloat16)
     k = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
 
@@ -94,7 +63,40 @@ def test_rollout_peek_needs_the_hip_library_on_cpu():
     saved = (sa.SEL.mode, sa.SEL.kernel_v2)
     try:
         sa.SEL.mode, sa.SEL.kernel_v2 = "rollout_peek", False
-        with pytest.raises((AssertionError, RuntimeError)):
+        with pytest.raises(NotImplementedError, match="rollout_peek"):
             sa.block_sparse_attention(M(), q, k, k, None, 0.125)
     finally:
         sa.SEL.mode, sa.SEL.kernel_v2 = saved
+
+
+@pytest.mark.parametrize("kernel_v2,mode", [(True, "router"), (True, "quest"),
+                                            (False, "topk"), (False, "router")])
+def test_sparse_paths_reject_query_shorter_than_keys(kernel_v2, mode):
+    """A query shorter than the keys (prefill continuing a cache) would need
+    shifted positions in the selector and the causal mask; like the
+    reference's launchers (q.shape == k.shape), the sparse paths refuse it
+    before touching any device."""
+    q = torch.zeros(1, 4, 64, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
+
+    class M:
+        num_key_value_groups, layer_idx = 2, 0
+    saved = (sa.SEL.mode, sa.SEL.kernel_v2)
+    try:
+        sa.SEL.mode, sa.SEL.kernel_v2 = mode, kernel_v2
+        with pytest.raises(AssertionError, match="query length"):
+            sa.block_sparse_attention(M(), q, k, k, None, 0.125)
+    finally:
+        sa.SEL.mode, sa.SEL.kernel_v2 = saved
+
+
+def test_launchers_reject_query_shorter_than_keys():
+    import block_attn
+    q = torch.zeros(1, 4, 64, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="query length"):
+        block_attn.block_sparse_attn_v2(q, k, k, torch.zeros(1, 4, 1, 2, dtype=torch.int32), 0.125)
+    with pytest.raises(AssertionError, match="query length"):
+        block_attn.block_sparse_attn(q, k, k, torch.ones(1, 4, 64, 2, dtype=torch.bool), 0.125)
+    with pytest.raises(AssertionError, match="query length"):
+        sa.select_v2(q, k, 0.125)

@@ -84,3 +84,38 @@ def test_compute_kv_idx_bruteforce():
             assert all(x == 5 for x in kv[0, h, t].tolist()[len(want):])
     kv0, mk0 = A.compute_kv_idx(np.zeros((1, 1, 64, 3), bool), 64)
     assert mk0 == 1 and kv0.tolist() == [[[[3]]]]
+
+
+def load_attention_golden():
+    """Cases written by tests/golden/make_golden_attn.py from the reference's
+    own reference_attn (src/triton_block_attn.py:301-312, CPU fp32)."""
+    import os
+    from conftest import GOLDEN, bf16_bits_to_f32
+    z = np.load(os.path.join(GOLDEN, "attention_reference.npz"))
+    cases = {}
+    for key in z.files:
+        name, field = key.split("/", 1)
+        cases.setdefault(name, {})[field] = z[key]
+    for c in cases.values():
+        for t in ("q", "k", "v"):
+            c[t] = bf16_bits_to_f32(c.pop(f"{t}_bf16"))
+    return cases
+
+
+def test_oracle_matches_reference_attn_golden():
+    """Both oracle formulations reproduce the reference's SDPA-with-mask output
+    on its own fixtures (dense, GQA + ragged tail, batch 2 at head_dim 256)."""
+    cases = load_attention_golden()
+    assert sorted(cases) == ["dense_d64", "gqa_ragged_d128", "multi_d256"]
+    for name, c in cases.items():
+        sc = float(c["scale"])
+        g = A.gathered_attention(c["q"], c["k"], c["v"], c["kv_idx"], sc)
+        m = A.masked_tile_attention(c["q"], c["k"], c["v"], c["kv_idx"], sc)
+        np.testing.assert_allclose(g, c["out"], atol=2e-6, err_msg=name)
+        np.testing.assert_allclose(m, c["out"], atol=2e-6, err_msg=name)
+        # a planted error would show: dropping the last listed block of one tile
+        kv = c["kv_idx"].copy()
+        nb = (c["k"].shape[2] + 63) // 64
+        row = kv[0, 0, -1]
+        row[np.flatnonzero(row < nb)[-1]] = nb                       # the sentinel: skipped
+        assert np.abs(A.gathered_attention(c["q"], c["k"], c["v"], kv, sc) - c["out"]).max() > 1e-3

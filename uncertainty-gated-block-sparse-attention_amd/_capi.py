@@ -60,7 +60,7 @@ SIGNATURES = {
                             _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f,
                             _p, _i64, _i64, _i64, _i64, _p, _p]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _LIB = None
 

@@ -16,6 +16,9 @@ the reference launchers, all additive:
   ``.contiguous()``); ``out`` may be any such strided view, which lets the
   dispatcher write the ``[B, S, H, D]`` layout directly.
 * ``num_warps`` / ``num_stages`` are Triton tuning knobs, accepted and ignored.
+* Both launchers assert query length == key length before anything else
+  (the reference asserts ``q.shape == k.shape``): the causal mask takes query
+  row i as key position i.
 * ``block_sparse_attn``: a query row whose keep mask selects no visible key
   gets a zero output (the reference kernel returns the mean of the masked
   values there); the selector never produces such rows (sink forced).
@@ -53,6 +56,7 @@ def block_sparse_attn_v2(q, k, v, kv_idx, scale, block_n=64, block_m=64,
     """
     assert q.dim() == 4 and k.shape == v.shape and q.shape[0] == k.shape[0] \
         and q.shape[-1] == k.shape[-1], "q [B,H,M,D], k = v [B,Hk,N,D] expected"
+    assert q.shape[2] == k.shape[2], "query length must equal key length (one-shot prefill)"
     assert q.is_cuda and kv_idx.dtype == torch.int32
     assert block_n == 64, "key blocks are 64 tokens"
     B, H, M, D = q.shape
@@ -116,6 +120,7 @@ def block_sparse_attn(q, k, v, keep, scale, block_n=64, block_m=64,
     """
     assert q.dim() == 4 and k.shape == v.shape and q.shape[0] == k.shape[0] \
         and q.shape[-1] == k.shape[-1], "q [B,H,M,D], k = v [B,Hk,N,D] expected"
+    assert q.shape[2] == k.shape[2], "query length must equal key length (one-shot prefill)"
     assert q.is_cuda and keep.dtype == torch.bool
     assert block_n == 64, "key blocks are 64 tokens"
     B, H, M, D = q.shape

@@ -21,20 +21,20 @@
 // keys, which makes the V^T operand eight consecutive keys of one column.
 //
 // Two kernels share this mapping:
-//   attn_fwd_pipe_kernel  64-row tiles at head_dim 64 / 128 (the default):
-//                         32-key half blocks, S of the next half block
-//                         computed while the softmax of the current one runs,
-//                         K / V^T read from an operand-order copy
-//                         (kv_operand_kernel) two half blocks ahead;
-//   attn_fwd_kernel       head_dim 256 and 32-row tiles: K read in place,
-//                         V^T from a per-block transposed copy
-//                         (v_block_transpose_kernel); launch shape selectable.
+//   attn_fwd_pipe_kernel  64-row tiles (attn_pipe.h; head_dim 64 / 128 here,
+//                         256 in attn_fwd256.hip): 32-key half blocks, S of
+//                         the next half block computed while the softmax of
+//                         the current one runs, K / V^T read from an
+//                         operand-order copy (kv_operand_kernel);
+//   attn_fwd_kernel       32-row tiles: K read in place, V^T from a
+//                         per-block transposed copy (v_block_transpose_kernel).
 //
-// Launch order: heaviest tiles first (t descending; a tile visits up to
-// min(t + 1, k_slots) blocks), and the G query heads of one (b, KV head, t)
-// are placed on the same XCD (workgroup i runs on XCD i % 8), so their
-// shared picks (sink, local, group needles) hit the same L2.
-#include <cstdio>
+// Launch order: the (b, t) tiles are ranked by their visited slots over all
+// query heads (tile_work_kernel + tile_order_kernel, heaviest first), and the
+// G query heads of one (b, KV head, t) are placed on the same XCD (workgroup
+// i runs on XCD i % 8), so their shared picks (sink, local, group needles)
+// hit the same L2; long contexts launch the units in generations
+// (attn_pipe.h, launch_attn_pipe).
 #include <cstdlib>
 
 #include "common.h"
@@ -131,6 +131,101 @@ __global__ __launch_bounds__(256) void kv_operand_kernel(
   }
 }
 
+// Work of each (b, t) tile of 64 query rows: the visited slots of its
+// kv_idx rows summed over the H query heads (slot values in [0, NB) and at
+// most t, the blocks the attention loop visits).  One wavefront per tile.
+__global__ __launch_bounds__(256) void tile_work_kernel(const int32_t* __restrict__ kv_idx,
+                                                        int64_t si_b, int64_t si_h, int64_t si_t,
+                                                        int B, int H, int Qt, int k_slots, int NB,
+                                                        int32_t* __restrict__ work) {
+  const int lane = threadIdx.x & 63;
+  const int bt = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (bt >= B * Qt) return;
+  const int b = bt / Qt, t = bt - b * Qt;
+  int cnt = 0;
+  for (int h = 0; h < H; ++h) {
+    const int32_t* row = kv_idx + b * si_b + h * si_h + t * si_t;
+    for (int s = lane; s < k_slots; s += 64) {
+      const int v = row[s];
+      cnt += (v >= 0 && v < NB && v <= t) ? 1 : 0;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+  if (lane == 0) work[bt] = cnt;
+}
+
+// The (b, t) tiles ordered by work, heaviest first: a stable counting sort
+// of the tiles, taken in the order t descending then b, by 16 work classes
+// (class = work * 16 / (max work + 1)).  One workgroup: each thread takes a
+// contiguous run of tiles, counts its classes, and after a scan over
+// (class, thread) writes its tiles to their places.  order[i] = b * Qt + t.
+constexpr int kOrderThreads = 512, kOrderClasses = 16;
+__global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
+    const int32_t* __restrict__ work, int B, int Qt, int32_t* __restrict__ order) {
+  __shared__ int32_t cnt[kOrderClasses][kOrderThreads];
+  __shared__ int32_t part[kOrderThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = B * Qt;
+  const int per = (n + kOrderThreads - 1) / kOrderThreads;
+  const int i0 = tid * per < n ? tid * per : n;
+  const int i1 = i0 + per < n ? i0 + per : n;
+  auto tile_at = [&](int i) -> int { return (i % B) * Qt + (Qt - 1 - i / B); };
+  // the largest work
+  int mx = 0;
+  for (int i = i0; i < i1; ++i) mx = max(mx, work[tile_at(i)]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) part[wave] = mx;
+  __syncthreads();
+  mx = 0;
+#pragma unroll
+  for (int w = 0; w < kOrderThreads / 64; ++w) mx = max(mx, part[w]);
+  auto cls = [&](int w) -> int {   // 0 = heaviest
+    return kOrderClasses - 1 - static_cast<int>(static_cast<int64_t>(w) * kOrderClasses / (mx + 1));
+  };
+#pragma unroll
+  for (int c = 0; c < kOrderClasses; ++c) cnt[c][tid] = 0;
+  for (int i = i0; i < i1; ++i) ++cnt[cls(work[tile_at(i)])][tid];
+  __syncthreads();
+  // exclusive scan of cnt in (class, thread) order: thread j sums the
+  // kOrderClasses consecutive counters [j * C, (j + 1) * C) of the flat array
+  int32_t* flat = &cnt[0][0];
+  int32_t loc[kOrderClasses];
+  int sum = 0;
+#pragma unroll
+  for (int c = 0; c < kOrderClasses; ++c) {
+    loc[c] = flat[tid * kOrderClasses + c];
+    sum += loc[c];
+  }
+  __syncthreads();   // part[] is reused below
+  const int excl = static_cast<int>(wave_excl_scan(static_cast<uint32_t>(sum), lane));
+  if (lane == 63) part[wave] = excl + sum;
+  __syncthreads();
+  int base = excl;
+  for (int w = 0; w < wave; ++w) base += part[w];
+#pragma unroll
+  for (int c = 0; c < kOrderClasses; ++c) {
+    flat[tid * kOrderClasses + c] = base;
+    base += loc[c];
+  }
+  __syncthreads();
+  for (int i = i0; i < i1; ++i) {
+    const int bt = tile_at(i);
+    order[cnt[cls(work[bt])][tid]++] = bt;
+  }
+}
+
+hipError_t launch_attn_tile_order(const int32_t* kv_idx, int64_t si_b, int64_t si_h,
+                                  int64_t si_t, int B, int H, int Qt, int k_slots, int NB,
+                                  int32_t* ws, hipStream_t stream) {
+  const int n = B * Qt;
+  tile_work_kernel<<<(n + 3) / 4, 256, 0, stream>>>(kv_idx, si_b, si_h, si_t, B, H, Qt, k_slots,
+                                                    NB, ws);
+  tile_order_kernel<<<1, kOrderThreads, 0, stream>>>(ws, B, Qt, ws + n);
+  return hipGetLastError();
+}
+
 // The pipelined kernel serves 64-row tiles (head_dim 64 / 128 here, 256 in
 // attn_fwd256.hip); 32-row tiles use attn_fwd_kernel, which reads K directly
 // and V^T per block.
@@ -171,30 +266,11 @@ __device__ __forceinline__ int key_of(int mt, int R) {
   return 32 * (mt >> 1) + 8 * (R >> 2) + 4 * (mt & 1) + (R & 3);
 }
 
-// Launch shape of the attention kernel:
-//   NT     16-row N-tiles per wave (a wave computes 16 * NT query rows);
-//   WPT    waves per workgroup; a workgroup owns one Q tile;
-//   SPLIT  true: every wave owns all 16 * NT rows of the tile and visits the
-//          slots s = wave (mod WPT); the partial (m, l, O) of the waves are
-//          merged through LDS at the end.  false: the waves own disjoint row
-//          slices (tile = 16 * NT * WPT rows) and all visit every slot;
-//   QLDS   Q fragments are staged once per tile in LDS and re-read per block
-//          (frees 16 * NT * D / 64 VGPRs) instead of being held in registers;
-//   PF     register prefetch: V^T of the current block is requested before
-//          its S^T product and K of the next visited block right after it.
-template <int D, int NT, int WPT, bool SPLIT, bool QLDS, bool PF>
-struct AttnShape {
-  static constexpr int BM = SPLIT ? 16 * NT : 16 * NT * WPT;
-  static constexpr int KS = D / 32;
-  static constexpr int DT = D / 16;
-  static constexpr int QROW = D + 8;                  // padded LDS row (bank-conflict free)
-  static constexpr int Q_BYTES = QLDS ? BM * QROW * 2 : 0;
-  static constexpr int PART = (DT * NT * 4 + 2 * NT) * 64;   // floats per merged wave
-  static constexpr int MERGE_BYTES = SPLIT ? (WPT - 1) * PART * 4 : 0;
-  static constexpr int LDS = Q_BYTES > MERGE_BYTES ? Q_BYTES : MERGE_BYTES;
-};
-
-template <int D, int NT, int WPT, bool SPLIT, bool QLDS, bool PF>
+// The 32-row tile kernel: a workgroup of WPT waves owns one Q tile of
+// 16 * NT * WPT = 32 rows, each wave 16 * NT of them, and every wave visits
+// every listed block.  V^T of the current block is requested before its S^T
+// product and K of the next visited block right after it.
+template <int D, int NT, int WPT>
 __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
@@ -202,9 +278,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     const uint64_t* __restrict__ rowmask, int64_t si_b, int64_t si_h, int64_t si_t, int B,
     int Hk, int M, int N, int NB, int Qt, int k_slots, float scale_signed,
     uint16_t* __restrict__ out, int64_t so_b, int64_t so_h, int64_t so_m, int units, int grp) {
-  using S = AttnShape<D, NT, WPT, SPLIT, QLDS, PF>;
-  constexpr int BM = S::BM, KS = S::KS, DT = S::DT;
-  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int BM = 16 * NT * WPT, KS = D / 32, DT = D / 16;
 
   // Workgroup -> (unit, head-in-group); a unit is one (t, b, KV head).
   const int wg = blockIdx.x;
@@ -222,37 +296,23 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g4 = lane >> 4, r16 = lane & 15;
-  const int row0 = t * BM + (SPLIT ? 0 : wave * 16 * NT);
+  const int row0 = t * BM + wave * 16 * NT;
   const uint16_t* qb = q + b * sq_b + h * sq_h;
   // A negative scale is moved onto Q (bf16 negation is exact), so the
   // softmax below always scales by scale_log2 > 0.
   const uint32_t qsign = scale_signed < 0.f ? 0x80008000u : 0u;
   const float scale_log2 = fabsf(scale_signed);
 
-  // ---- Q (B operand of S^T): registers or LDS ---------------------------
-  bf16x8 qf[QLDS ? 1 : NT][QLDS ? 1 : KS];
-  uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
-  if constexpr (QLDS) {
-    constexpr int CH = D / 8;
-    for (int pi = threadIdx.x; pi < BM * CH; pi += 64 * WPT) {
-      const int r = pi / CH, c = pi % CH;
-      const int row = t * BM + r;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (row < M) val = *reinterpret_cast<const u32x4*>(qb + row * sq_m + c * 8) ^ qsign;
-      *reinterpret_cast<u32x4*>(qs + r * S::QROW + c * 8) = val;
-    }
-    __syncthreads();
-  } else {
+  // ---- Q (B operand of S^T) in registers ---------------------------------
+  bf16x8 qf[NT][KS];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int row = row0 + 16 * nt + r16;
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = row0 + 16 * nt + r16;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        qf[nt][ks] = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
-                             : zero_bf16x8();
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      qf[nt][ks] = row < M ? __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)) ^ qsign)
+                           : zero_bf16x8();
   }
-  const int qlds_row0 = (row0 - t * BM) + r16;    // this lane's first row inside the tile
 
   f32x4 o[DT][NT];
 #pragma unroll
@@ -281,12 +341,11 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     koff[mt] = static_cast<uint32_t>(key_of(mt, r16) * sk_n * 2 + g4 * 16);
   const uint32_t voff = static_cast<uint32_t>(r16 * kBlock * 2 + g4 * 16);
   const int q_last = t * BM + BM - 1;
-  constexpr int step = SPLIT ? WPT : 1;
 
   auto block_at = [&](int s) -> int { return __builtin_amdgcn_readfirstlane(idx[s]); };
   auto visits = [&](int blk) -> bool { return blk >= 0 && blk < NB && blk * kBlock <= q_last; };
   auto next_slot = [&](int s) -> int {
-    while (s < k_slots && !visits(block_at(s))) s += step;
+    while (s < k_slots && !visits(block_at(s))) ++s;
     return s;
   };
   auto load_k = [&](int blk, bf16x8 (&kf)[4][KS]) {
@@ -301,22 +360,18 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
                               static_cast<uint32_t>(blk * D * kBlock * 2));
   };
 
-  int s = next_slot(SPLIT ? wave : 0);
+  int s = next_slot(0);
   bf16x8 kf[4][KS];
-  if (PF && s < k_slots) load_k(block_at(s), kf);
+  if (s < k_slots) load_k(block_at(s), kf);
 
   while (s < k_slots) {
     const int blk = block_at(s);
     const int kbase = blk * kBlock;
-    bf16x8 vf[PF ? DT : 1][2];
-    if constexpr (PF) {
+    bf16x8 vf[DT][2];
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) vf[dt][s2] = load_v(blk, dt, s2);
-    } else {
-      load_k(blk, kf);
-    }
+      for (int s2 = 0; s2 < 2; ++s2) vf[dt][s2] = load_v(blk, dt, s2);
 
     // ---- S^T = K . Q^T -------------------------------------------------
     f32x4 st[4][NT];
@@ -325,20 +380,14 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) st[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      bf16x8 qv[NT];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        qv[nt] = QLDS ? *reinterpret_cast<const bf16x8*>(qs + (qlds_row0 + 16 * nt) * S::QROW + 32 * ks + 8 * g4)
-                      : qf[QLDS ? 0 : nt][QLDS ? 0 : ks];
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) st[mt][nt] = mfma16x16x32(kf[mt][ks], qv[nt], st[mt][nt]);
-    }
+        for (int nt = 0; nt < NT; ++nt) st[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], st[mt][nt]);
 
-    const int s_next = next_slot(s + step);
-    if (PF && s_next < k_slots) load_k(block_at(s_next), kf);
+    const int s_next = next_slot(s + 1);
+    if (s_next < k_slots) load_k(block_at(s_next), kf);
 
     // ---- causal / bounds / row-keep mask, online softmax (log2 domain) ---
     uint64_t mk = ~0ull;
@@ -412,7 +461,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 vv = PF ? vf[PF ? dt : 0][s2] : load_v(blk, dt, s2);
+        const bf16x8 vv = vf[dt][s2];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) o[dt][nt] = mfma16x16x32(vv, pb[nt], o[dt][nt]);
       }
@@ -420,50 +469,9 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     s = s_next;
   }
 
-  // ---- row sums, cross-wave merge (SPLIT), normalise and store ----------
+  // ---- row sums, normalise and store ------------------------------------
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    l[nt] = quad_rows_sum(l[nt]);
-  }
-  if constexpr (SPLIT) {
-    float* part = reinterpret_cast<float*>(smem);
-    __syncthreads();                       // every wave is done with the Q tile in LDS
-    if (wave > 0) {
-      float* my = part + (wave - 1) * S::PART;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) my[((dt * NT + nt) * 4 + i) * 64 + lane] = o[dt][nt][i];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        my[(DT * NT * 4 + nt) * 64 + lane] = m[nt];
-        my[(DT * NT * 4 + NT + nt) * 64 + lane] = l[nt];
-      }
-    }
-    __syncthreads();
-    if (wave > 0) return;
-#pragma unroll
-    for (int w = 1; w < WPT; ++w) {
-      const float* pw = part + (w - 1) * S::PART;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float mw = pw[(DT * NT * 4 + nt) * 64 + lane];
-        const float lw = pw[(DT * NT * 4 + NT + nt) * 64 + lane];
-        const float mn = fmaxf(m[nt], mw);
-        const float a0 = __builtin_amdgcn_exp2f(m[nt] - mn);
-        const float a1 = __builtin_amdgcn_exp2f(mw - mn);
-        m[nt] = mn;
-        l[nt] = l[nt] * a0 + lw * a1;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            o[dt][nt][i] = o[dt][nt][i] * a0 + pw[((dt * NT + nt) * 4 + i) * 64 + lane] * a1;
-      }
-    }
-  }
+  for (int nt = 0; nt < NT; ++nt) l[nt] = quad_rows_sum(l[nt]);
 
   uint16_t* ob = out + b * so_b + h * so_h;
 #pragma unroll
@@ -481,7 +489,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
   }
 }
 
-template <int D, int NT, int WPT, bool SPLIT, bool QLDS, bool PF>
+template <int D, int NT, int WPT>
 static hipError_t launch_attn_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                 const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                                 const uint16_t* vt, const int32_t* kv_idx,
@@ -489,43 +497,15 @@ static hipError_t launch_attn_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, i
                                 int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
                                 int k_slots, float scale, uint16_t* out, int64_t so_b,
                                 int64_t so_h, int64_t so_m, hipStream_t stream) {
-  using S = AttnShape<D, NT, WPT, SPLIT, QLDS, PF>;
   const int NB = (N + kBlock - 1) / kBlock;
   const int grp = H / Hk;
   const int units = B * Hk * Qt;
   const int64_t wgs = 8LL * grp * ((units + 7) / 8);
-  auto kern = attn_fwd_kernel<D, NT, WPT, SPLIT, QLDS, PF>;
-  if (S::LDS > 64 * 1024)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS);
-  kern<<<dim3(static_cast<unsigned>(wgs)), 64 * WPT, S::LDS, stream>>>(
+  attn_fwd_kernel<D, NT, WPT><<<dim3(static_cast<unsigned>(wgs)), 64 * WPT, 0, stream>>>(
       q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, Hk, M,
       N, NB, Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
   return hipGetLastError();
 }
-
-// Attention launch shapes, per (head_dim, tile rows).  The first entry of each
-// group is the default; UGBSA_ATTN_VARIANT="NT,WPT,SPLIT,QLDS,PF" picks
-// another compiled entry (tuning sweeps).
-struct AttnVariant {
-  int D, block_m, NT, WPT, SPLIT, QLDS, PF;
-};
-#define UGBSA_ATTN_VARIANTS(X)   \
-  X(128, 64, 4, 1, 0, 0, 1)     \
-  X(128, 64, 4, 1, 0, 0, 0)     \
-  X(128, 64, 4, 2, 1, 1, 1)     \
-  X(128, 64, 4, 2, 1, 1, 0)     \
-  X(128, 64, 2, 2, 0, 0, 1)     \
-  X(128, 64, 2, 2, 0, 1, 1)     \
-  X(128, 64, 4, 4, 1, 1, 0)     \
-  X(64, 64, 4, 1, 0, 0, 1)      \
-  X(64, 64, 4, 2, 1, 1, 1)      \
-  X(256, 64, 2, 2, 0, 0, 1)     \
-  X(256, 64, 2, 2, 0, 1, 1)     \
-  X(256, 64, 2, 2, 0, 1, 0)     \
-  X(64, 32, 2, 1, 0, 0, 1)      \
-  X(128, 32, 2, 1, 0, 0, 1)     \
-  X(256, 32, 1, 2, 0, 0, 1)
 
 hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                            const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
@@ -533,16 +513,21 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
                            int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
                            int D, int Qt, int k_slots, int block_m, float scale, uint16_t* out,
                            int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream,
-                           const uint64_t* rowmask) {
-  int want[5] = {-1, -1, -1, -1, -1};
-  if (const char* env = getenv("UGBSA_ATTN_VARIANT"))
-    sscanf(env, "%d,%d,%d,%d,%d", &want[0], &want[1], &want[2], &want[3], &want[4]);
+                           const uint64_t* rowmask, int32_t* order_ws) {
   if (uses_pipe(D, block_m)) {   // the pipelined kernel (its K/V operand layout is prepared)
     if (k_slots > kPipeMaxSlots) return hipErrorInvalidValue;
+    const int NBk = (N + kBlock - 1) / kBlock;
+    const int32_t* tile_order = nullptr;
+    if (order_ws != nullptr) {
+      hipError_t e = launch_attn_tile_order(kv_idx, si_b, si_h, si_t, B, H, Qt, k_slots, NBk,
+                                            order_ws, stream);
+      if (e != hipSuccess) return e;
+      tile_order = order_ws + static_cast<int64_t>(B) * Qt;
+    }
     if (D == 256)
       return launch_attn_pipe256(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b,
                                  si_h, si_t, B, H, Hk, M, N, Qt, k_slots, scale, out, so_b, so_h,
-                                 so_m, stream);
+                                 so_m, stream, tile_order);
     // the single-set prefetch above kPipeLongBlocks context blocks;
     // UGBSA_PIPE_LONG=0/1 forces either variant (tests)
     const char* lv = getenv("UGBSA_PIPE_LONG");
@@ -550,30 +535,26 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
     if (D == 128 && long_ctx)
       return launch_attn_pipe128_long(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                       rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
-                                      scale, out, so_b, so_h, so_m, stream);
+                                      scale, out, so_b, so_h, so_m, stream, tile_order);
     if (D == 128)
       return launch_attn_pipe<128, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                           rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
-                                          scale, out, so_b, so_h, so_m, stream);
+                                          scale, out, so_b, so_h, so_m, stream, tile_order);
     return launch_attn_pipe<64, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                        rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
-                                       scale, out, so_b, so_h, so_m, stream);
+                                       scale, out, so_b, so_h, so_m, stream, tile_order);
   }
-  bool first = true;
-#define UGBSA_TRY(D_, BM_, NT_, WPT_, SP_, QL_, PF_)                                            \
-  if (D == D_ && block_m == BM_) {                                                             \
-    const bool match = want[0] < 0 ? first                                                     \
-        : (want[0] == NT_ && want[1] == WPT_ && want[2] == SP_ && want[3] == QL_ && want[4] == PF_); \
-    first = false;                                                                             \
-    if (match)                                                                                 \
-      return launch_attn_t<D_, NT_, WPT_, SP_ != 0, QL_ != 0, PF_ != 0>(                        \
-          q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, H, \
-          Hk, M, N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream);                        \
+  // 32-row tiles: the older kernel (K read in place, V^T per block)
+  if (block_m != 32) return hipErrorInvalidValue;
+#define UGBSA_ATTN32_ARGS                                                                     \
+  q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, H, Hk, M, \
+      N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream
+  switch (D) {
+    case 64: return launch_attn_t<64, 2, 1>(UGBSA_ATTN32_ARGS);
+    case 128: return launch_attn_t<128, 2, 1>(UGBSA_ATTN32_ARGS);
+    case 256: return launch_attn_t<256, 1, 2>(UGBSA_ATTN32_ARGS);
   }
-  {
-    UGBSA_ATTN_VARIANTS(UGBSA_TRY)
-  }
-#undef UGBSA_TRY
+#undef UGBSA_ATTN32_ARGS
   return hipErrorInvalidValue;
 }
 

@@ -18,11 +18,12 @@ hipError_t launch_attn_pipe128_long(const uint16_t* q, int64_t sq_b, int64_t sq_
                                     const uint64_t* rowmask, int64_t si_b, int64_t si_h,
                                     int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
                                     int k_slots, float scale, uint16_t* out, int64_t so_b,
-                                    int64_t so_h, int64_t so_m, hipStream_t stream) {
+                                    int64_t so_h, int64_t so_m, hipStream_t stream,
+                                    const int32_t* tile_order) {
   return launch_attn_pipe<128, 4, false, true>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt,
                                                kv_idx, rowmask, si_b, si_h, si_t, B, H, Hk, M,
                                                N, Qt, k_slots, scale, out, so_b, so_h, so_m,
-                                               stream);
+                                               stream, tile_order);
 }
 
 }  // namespace ugbsa

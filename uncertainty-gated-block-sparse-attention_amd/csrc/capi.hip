@@ -52,6 +52,14 @@ int check_dims(int B, int H, int Hk, int D, int dtype) {
   return UGBSA_OK;
 }
 
+// bf16 elements of the K and V operand copies in the attention workspace;
+// the tile schedule (2 * B * NB int32: per-tile work, then the tile order)
+// follows them.
+int64_t kv_copy_elems(int B, int Hk, int N, int D) {
+  const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  return 2 * static_cast<int64_t>(B) * Hk * nb * ugbsa::kBlock * D;
+}
+
 }  // namespace
 
 extern "C" {
@@ -67,7 +75,8 @@ int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode) {
 
 int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D) {
   const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
-  return 2 * static_cast<int64_t>(B) * Hk * nb * ugbsa::kBlock * D;   // K and V operand copies
+  const int64_t sched = (4 * static_cast<int64_t>(B) * nb + 7) / 8 * 8;   // 2 B NB int32
+  return kv_copy_elems(B, Hk, N, D) + sched;
 }
 
 int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
@@ -93,6 +102,8 @@ int ugbsa_select(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_
   if (rc) return rc;
   if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
   if (M < 1 || N < 1) return fail(UGBSA_EARG, "M and N must be positive");
+  // tile visibility takes query row i as key position i (one-shot prefill)
+  if (M != N) return fail(UGBSA_EARG, "selection needs query length == key length (M=%d, N=%d)", M, N);
   if (block_m != 64) return fail(UGBSA_EARG, "selection tiles are 64 rows (block_m=%d)", block_m);
   if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
   if (planes == nullptr || kv_idx == nullptr) return fail(UGBSA_EARG, "planes / kv_idx is null");
@@ -180,7 +191,7 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
   if (N < 1) return fail(UGBSA_EARG, "N must be positive");
   if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
   if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace must be a 16-byte aligned buffer");
-  if (ugbsa_attn_workspace_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
+  if (kv_copy_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
     return fail(UGBSA_EARG, "one KV head's K/V copy exceeds 4 GiB (N=%d, D=%d)", N, D);
   return hip_result(ugbsa::launch_attn_prepare(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n,
                                                static_cast<const uint16_t*>(v), sv_b, sv_h, sv_n,
@@ -193,6 +204,68 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
 }  // extern "C"
 
 namespace {
+
+int select_mask_impl(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
+                      const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
+                      int mode, float scaling, int policy, int k_bud, int k_eff, int k_min,
+                      int k_max, float top_p, const float* penalty, float* workspace,
+                      int64_t workspace_elems, uint8_t* keep, float* margin, void* stream) {
+  int rc = check_dims(B, H, Hk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
+  if (M < 1 || M != N) return fail(UGBSA_EARG, "the per-row selector needs M == N >= 1 (M=%d, N=%d)", M, N);
+  if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
+  if (policy != UGBSA_V1_TOPK && policy != UGBSA_V1_BELIEF) return fail(UGBSA_EARG, "unknown v1 policy %d", policy);
+  if (planes == nullptr || !aligned16(planes)) return fail(UGBSA_ELAYOUT, "planes must be a 16-byte aligned buffer");
+  if (keep == nullptr) return fail(UGBSA_EARG, "keep is null");
+  const int nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  if (nb > ugbsa::kStreamBlocksRows) return fail(UGBSA_EARG, "N=%d gives %d key blocks; the per-row selector holds at most %d", N, nb, ugbsa::kStreamBlocksRows);
+  if (k_eff < 0 || k_eff >= nb) return fail(UGBSA_EARG, "k_eff=%d out of range [0, NB=%d)", k_eff, nb);
+  if (k_eff > 0 && margin == nullptr) return fail(UGBSA_EARG, "margin is null (k_eff > 0)");
+  int K;
+  if (policy == UGBSA_V1_BELIEF) {
+    if (k_min < 0 || k_max < 1 || !(top_p == top_p)) return fail(UGBSA_EARG, "belief needs k_max >= 1 and a top_p");
+    K = k_max < nb ? k_max : nb;
+  } else {
+    if (k_bud < 1 || k_bud > nb) return fail(UGBSA_EARG, "k_bud=%d out of range [1, NB=%d]", k_bud, nb);
+    K = k_bud;
+  }
+  if (k_eff + 1 > K) K = k_eff + 1;
+  if (K > ugbsa::kMaxSlots) return fail(UGBSA_EARG, "ranking %d blocks deep exceeds %d", K, ugbsa::kMaxSlots);
+  const int64_t per_row = static_cast<int64_t>(B) * H * nb;
+  const int64_t chunk_tiles = workspace_elems / (per_row * ugbsa::kBlock);
+  if (chunk_tiles < 1) return fail(UGBSA_EARG, "workspace of %lld floats holds less than one 64-row tile (%lld)", (long long)workspace_elems, (long long)(per_row * ugbsa::kBlock));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Qt = (M + ugbsa::kBlock - 1) / ugbsa::kBlock;
+  for (int t0 = 0; t0 < Qt; t0 += static_cast<int>(chunk_tiles)) {
+    const int t1 = t0 + static_cast<int>(chunk_tiles) < Qt ? t0 + static_cast<int>(chunk_tiles) : Qt;
+    ugbsa::SelectAux aux;
+    aux.row_scores = workspace;
+    aux.rows_t0 = t0;
+    aux.rows_t1 = t1;
+    hipError_t e = ugbsa::launch_select(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
+                                        static_cast<const uint16_t*>(planes), B, H, Hk, M, N, D,
+                                        mode, scaling, 1, 1, 0, nullptr, nullptr, nullptr, st, &aux);
+    if (e != hipSuccess) return hip_result(e, "select_mask row scores");
+    ugbsa::RowsArgs a;
+    a.scores = workspace;
+    a.r0 = t0 * ugbsa::kBlock;
+    a.nrows = (t1 - t0) * ugbsa::kBlock;
+    a.B = B; a.H = H; a.M = M; a.NB = nb;
+    a.K = K;
+    a.k_bud = k_bud;
+    a.belief = policy == UGBSA_V1_BELIEF;
+    a.top_p = top_p;
+    a.k_min = k_min; a.k_max = k_max;
+    a.k_eff = k_eff;
+    a.penalty = penalty;
+    a.keep = keep;
+    a.margin = k_eff > 0 ? margin : nullptr;
+    e = ugbsa::launch_select_rows(a, st);
+    if (e != hipSuccess) return hip_result(e, "select_mask rows");
+  }
+  return hip_result(hipSuccess, "select_mask");
+}
 
 int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
                     const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
@@ -213,13 +286,15 @@ int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int
   if (kv_idx == nullptr || si_s != 1) return fail(UGBSA_ELAYOUT, "kv_idx must be non-null with unit slot stride");
   if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace (V block transpose) must be a 16-byte aligned buffer");
   if (M < 1 || N < 1) return fail(UGBSA_EARG, "M and N must be positive");
+  // the causal mask takes query row i as key position i (one-shot prefill)
+  if (M != N) return fail(UGBSA_EARG, "attention needs query length == key length (M=%d, N=%d)", M, N);
   if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
   if (Qt != (M + block_m - 1) / block_m) return fail(UGBSA_EARG, "kv_idx holds %d tiles, M=%d needs %d", Qt, M, (M + block_m - 1) / block_m);
   if (k_slots < 1) return fail(UGBSA_EARG, "k_slots must be positive");
   if (!(scale != 0.f && scale - scale == 0.f)) return fail(UGBSA_EARG, "scale must be finite and nonzero");
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* vt = static_cast<uint16_t*>(workspace);
-  if (static_cast<int64_t>(N) * sk_n * 2 > 0xFFFFFFFFLL || ugbsa_attn_workspace_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
+  if (static_cast<int64_t>(N) * sk_n * 2 > 0xFFFFFFFFLL || kv_copy_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
     return fail(UGBSA_EARG, "one KV head's K rows exceed the 4 GiB buffer-load range");
   if (k_slots > 16384 && block_m == 64 && D <= 128)
     return fail(UGBSA_EARG, "k_slots=%d exceeds the 16384-slot kv list of the attention kernel", k_slots);
@@ -235,7 +310,8 @@ int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int
                                            static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, vt,
                                            kv_idx, si_b, si_h, si_t, B, H, Hk, M, N, D, Qt,
                                            k_slots, block_m, scale, static_cast<uint16_t*>(out),
-                                           so_b, so_h, so_m, st, rowmask),
+                                           so_b, so_h, so_m, st, rowmask,
+                                           reinterpret_cast<int32_t*>(vt + kv_copy_elems(B, Hk, N, D))),
                     "attn_fwd");
 }
 
@@ -293,61 +369,10 @@ int ugbsa_select_mask(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, i
                       int mode, float scaling, int policy, int k_bud, int k_eff, int k_min,
                       int k_max, float top_p, const float* penalty, float* workspace,
                       int64_t workspace_elems, uint8_t* keep, float* margin, void* stream) {
-  int rc = check_dims(B, H, Hk, D, dtype);
-  if (rc) return rc;
-  if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
-  if (M < 1 || M != N) return fail(UGBSA_EARG, "the per-row selector needs M == N >= 1 (M=%d, N=%d)", M, N);
-  if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
-  if (policy != UGBSA_V1_TOPK && policy != UGBSA_V1_BELIEF) return fail(UGBSA_EARG, "unknown v1 policy %d", policy);
-  if (planes == nullptr || !aligned16(planes)) return fail(UGBSA_ELAYOUT, "planes must be a 16-byte aligned buffer");
-  if (keep == nullptr || workspace == nullptr) return fail(UGBSA_EARG, "keep / workspace is null");
-  const int nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
-  if (nb > ugbsa::kStreamBlocksRows) return fail(UGBSA_EARG, "N=%d gives %d key blocks; the per-row selector holds at most %d", N, nb, ugbsa::kStreamBlocksRows);
-  if (k_eff < 0 || k_eff >= nb) return fail(UGBSA_EARG, "k_eff=%d out of range [0, NB=%d)", k_eff, nb);
-  if (k_eff > 0 && margin == nullptr) return fail(UGBSA_EARG, "margin is null (k_eff > 0)");
-  int K;
-  if (policy == UGBSA_V1_BELIEF) {
-    if (k_min < 0 || k_max < 1 || !(top_p == top_p)) return fail(UGBSA_EARG, "belief needs k_max >= 1 and a top_p");
-    K = k_max < nb ? k_max : nb;
-  } else {
-    if (k_bud < 1 || k_bud > nb) return fail(UGBSA_EARG, "k_bud=%d out of range [1, NB=%d]", k_bud, nb);
-    K = k_bud;
-  }
-  if (k_eff + 1 > K) K = k_eff + 1;
-  if (K > ugbsa::kMaxSlots) return fail(UGBSA_EARG, "ranking %d blocks deep exceeds %d", K, ugbsa::kMaxSlots);
-  const int64_t per_row = static_cast<int64_t>(B) * H * nb;
-  const int64_t chunk_tiles = workspace_elems / (per_row * ugbsa::kBlock);
-  if (chunk_tiles < 1) return fail(UGBSA_EARG, "workspace of %lld floats holds less than one 64-row tile (%lld)", (long long)workspace_elems, (long long)(per_row * ugbsa::kBlock));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int Qt = (M + ugbsa::kBlock - 1) / ugbsa::kBlock;
-  for (int t0 = 0; t0 < Qt; t0 += static_cast<int>(chunk_tiles)) {
-    const int t1 = t0 + static_cast<int>(chunk_tiles) < Qt ? t0 + static_cast<int>(chunk_tiles) : Qt;
-    ugbsa::SelectAux aux;
-    aux.row_scores = workspace;
-    aux.rows_t0 = t0;
-    aux.rows_t1 = t1;
-    hipError_t e = ugbsa::launch_select(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
-                                        static_cast<const uint16_t*>(planes), B, H, Hk, M, N, D,
-                                        mode, scaling, 1, 1, 0, nullptr, nullptr, nullptr, st, &aux);
-    if (e != hipSuccess) return hip_result(e, "select_mask row scores");
-    ugbsa::RowsArgs a;
-    a.scores = workspace;
-    a.r0 = t0 * ugbsa::kBlock;
-    a.nrows = (t1 - t0) * ugbsa::kBlock;
-    a.B = B; a.H = H; a.M = M; a.NB = nb;
-    a.K = K;
-    a.k_bud = k_bud;
-    a.belief = policy == UGBSA_V1_BELIEF;
-    a.top_p = top_p;
-    a.k_min = k_min; a.k_max = k_max;
-    a.k_eff = k_eff;
-    a.penalty = penalty;
-    a.keep = keep;
-    a.margin = k_eff > 0 ? margin : nullptr;
-    e = ugbsa::launch_select_rows(a, st);
-    if (e != hipSuccess) return hip_result(e, "select_mask rows");
-  }
-  return hip_result(hipSuccess, "select_mask");
+  if (workspace == nullptr) return fail(UGBSA_EARG, "workspace is null");
+  return select_mask_impl(q, sq_b, sq_h, sq_m, sq_d, planes, B, H, Hk, M, N, D, dtype, mode,
+                          scaling, policy, k_bud, k_eff, k_min, k_max, top_p, penalty, workspace,
+                          workspace_elems, keep, margin, stream);
 }
 
 int ugbsa_router_rows(const float* margin, int B, int H, int M, int NB, int grain, int rmode,

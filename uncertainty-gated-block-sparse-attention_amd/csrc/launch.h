@@ -104,7 +104,14 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
                            int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
                            int D, int Qt, int k_slots, int block_m, float scale, uint16_t* out,
                            int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream,
-                           const uint64_t* rowmask = nullptr);
+                           const uint64_t* rowmask = nullptr, int32_t* order_ws = nullptr);
+
+// The (b, t) tiles of a kv_idx [B, H, Qt, k_slots] ordered by their visited
+// slots over all query heads, heaviest first (64-row tiles): ws holds 2 * B *
+// Qt int32 — the per-tile work, then the order (b * Qt + t per entry).
+hipError_t launch_attn_tile_order(const int32_t* kv_idx, int64_t si_b, int64_t si_h,
+                                  int64_t si_t, int B, int H, int Qt, int k_slots, int NB,
+                                  int32_t* ws, hipStream_t stream);
 
 // The pipelined attention kernel at head_dim 256 (attn_fwd256.hip: two
 // 32-row wavefronts per tile, Q in LDS, one K / V^T set per wavefront).
@@ -114,7 +121,8 @@ hipError_t launch_attn_pipe256(const uint16_t* q, int64_t sq_b, int64_t sq_h, in
                                const uint64_t* rowmask, int64_t si_b, int64_t si_h,
                                int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
                                int k_slots, float scale, uint16_t* out, int64_t so_b,
-                               int64_t so_h, int64_t so_m, hipStream_t stream);
+                               int64_t so_h, int64_t so_m, hipStream_t stream,
+                               const int32_t* tile_order);
 
 // The pipelined attention kernel at head_dim 128 with one K / V^T set
 // requested a phase ahead (attn_fwd_long.hip), for contexts of more than
@@ -126,7 +134,8 @@ hipError_t launch_attn_pipe128_long(const uint16_t* q, int64_t sq_b, int64_t sq_
                                     const uint64_t* rowmask, int64_t si_b, int64_t si_h,
                                     int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
                                     int k_slots, float scale, uint16_t* out, int64_t so_b,
-                                    int64_t so_h, int64_t so_m, hipStream_t stream);
+                                    int64_t so_h, int64_t so_m, hipStream_t stream,
+                                    const int32_t* tile_order);
 
 // _compute_kv_idx on the GPU: per (b, h, block_m-row tile) the blocks any row
 // of keep [B, H, M, NB] (uint8, contiguous) keeps, ascending, NB-padded to

@@ -30,73 +30,86 @@ import sparse_attention
 
 BLOCK = sparse_attention.BLOCK
 
-_STATE = {
-    "enabled": False,
-    "out_path": None,
-    "orig_fn": None,
-    "shards": [],
-    "call_idx": 0,
-}
-
 MODE_LABELS = {0: "topk", 1: "router_mean", 2: "router_quest", 3: "quest", 4: "other"}
 
 
 def _mode_id(sel) -> int:
-    """0=topk, 1=router-mean, 2=router-quest, 3=quest, 4=other (:210-219)."""
-    if sel.mode == "topk":
-        return 0
-    if sel.mode == "router":
-        return 2 if sel.router_score == "quest" else 1
+    """The shard's policy code: 0 topk, 1 router on K-mean, 2 router on Quest,
+    3 quest, anything else 4 (src/dump_block_scores.py:210-219)."""
+    codes = {("topk", False): 0, ("router", False): 1, ("router", True): 2}
     if sel.mode == "quest":
         return 3
-    return 4
+    return codes.get((sel.mode, sel.mode == "router" and sel.router_score == "quest"), 4)
+
+
+class _DumpSession:
+    """One recording session: the selector it wraps, the shards recorded so
+    far and where they go.  Only one session is active at a time."""
+
+    def __init__(self, out_path, inner):
+        self.out_path = out_path
+        self.inner = inner          # the selector function that was bound before
+        self.shards = []
+        self.calls = 0              # selection calls seen (recorded or not)
+        self.active = True          # False once torn down: the recorder only forwards
+
+    def selector(self, query, key_states, scaling, block_m=64):
+        """Stands in for ``sparse_attention._block_select_kv_idx_v2``: runs the
+        wrapped selector, then records a shard beside it.  The selection is
+        returned untouched; a recording failure is printed, not raised."""
+        kv_idx = self.inner(query, key_states, scaling, block_m=block_m)
+        if not self.active:
+            return kv_idx
+        try:
+            shard = record(query, key_states, scaling, block_m)
+        except Exception as err:   # the prefill must go on
+            print(f"[dump_block_scores] call {self.calls}: no shard ({type(err).__name__}: {err})",
+                  flush=True)
+        else:
+            if shard is not None:
+                shard["call_idx"] = self.calls
+                self.shards.append(shard)
+        self.calls += 1
+        return kv_idx
+
+    def write(self):
+        if not self.shards or self.out_path is None:
+            return
+        with open(self.out_path, "wb") as fh:
+            pickle.dump(self.shards, fh, protocol=pickle.HIGHEST_PROTOCOL)
+        cells = sum(int(sh["g"].size) for sh in self.shards)
+        print(f"[dump_block_scores] {len(self.shards)} shards, {cells} (B,H,Qt) cells -> "
+              f"{self.out_path}", flush=True)
+
+
+_session: _DumpSession | None = None
 
 
 def install_dump_hook(out_path):
-    """Wrap ``sparse_attention._block_select_kv_idx_v2`` so each call records
-    one shard (:57-71).  A second install is a no-op."""
-    if _STATE["enabled"]:
-        print(f"[dump_block_scores] already installed (out={_STATE['out_path']}); "
-              f"ignoring install with out={out_path}", flush=True)
+    """Start recording: rebind ``sparse_attention._block_select_kv_idx_v2``
+    (the dispatcher looks the name up at call time) to a recorder around the
+    current selector (src/dump_block_scores.py:57-71).  While a session is
+    active, another install changes nothing."""
+    global _session
+    if _session is not None:
+        print(f"[dump_block_scores] a session writing to {_session.out_path} is active; "
+              f"not installing another for {out_path}", flush=True)
         return
-    _STATE.update(orig_fn=sparse_attention._block_select_kv_idx_v2, out_path=out_path,
-                  shards=[], call_idx=0, enabled=True)
-    sparse_attention._block_select_kv_idx_v2 = _wrapped
-    print(f"[dump_block_scores] installed, dumping to {out_path}", flush=True)
+    _session = _DumpSession(out_path, sparse_attention._block_select_kv_idx_v2)
+    sparse_attention._block_select_kv_idx_v2 = _session.selector
+    print(f"[dump_block_scores] recording selection calls for {out_path}", flush=True)
 
 
 def flush_and_teardown():
-    """Restore the selector and write the shards to ``out_path`` (:74-80)."""
-    if not _STATE["enabled"]:
+    """End the session: bind the selector back and write the shards as one
+    pickled list (src/dump_block_scores.py:74-89).  No-op without a session."""
+    global _session
+    if _session is None:
         return
-    sparse_attention._block_select_kv_idx_v2 = _STATE["orig_fn"]
-    _STATE["enabled"] = False
-    _flush()
-
-
-def _flush():
-    if not _STATE["shards"] or _STATE["out_path"] is None:
-        return
-    with open(_STATE["out_path"], "wb") as f:
-        pickle.dump(_STATE["shards"], f, protocol=pickle.HIGHEST_PROTOCOL)
-    n_tiles = sum(s["g"].size for s in _STATE["shards"])
-    print(f"[dump_block_scores] wrote {len(_STATE['shards'])} calls "
-          f"({n_tiles} (B,H,Qt) cells) → {_STATE['out_path']}", flush=True)
-
-
-def _wrapped(query, key_states, scaling, block_m=64):
-    out = _STATE["orig_fn"](query, key_states, scaling, block_m=block_m)
-    if _STATE["enabled"]:
-        try:
-            shard = record(query, key_states, scaling, block_m)
-            if shard is not None:
-                shard["call_idx"] = _STATE["call_idx"]
-                _STATE["shards"].append(shard)
-        except Exception as e:   # never crash the prefill
-            print(f"[dump_block_scores] WARN record failed at call "
-                  f"{_STATE['call_idx']}: {type(e).__name__}: {e}", flush=True)
-        _STATE["call_idx"] += 1
-    return out
+    session, _session = _session, None
+    session.active = False
+    sparse_attention._block_select_kv_idx_v2 = session.inner
+    session.write()
 
 
 def dump_budgets(budget_blocks, n_blocks):

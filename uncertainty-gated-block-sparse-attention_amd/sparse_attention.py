@@ -33,16 +33,17 @@ Differences from the reference, by design:
   order, so rows with fewer visible blocks than the budget keep the lowest
   invisible blocks (the reference keeps arbitrary ones; attention never
   reads them).
-* ``rollout_peek`` (:386-583) takes its baseline top-k keep mask and the
-  fp32 block scores from the same HIP selection kernels; the planner around
-  them (a depth-1 forward of the model's own layers per candidate set, one
-  candidate at a time as the reference does) runs as torch calls on the
-  device, with un-repeated GQA key/value heads.
+* ``rollout_peek`` (:386-583) is not provided: it is an abandoned research
+  mode of the reference, off its v2 path (a depth-1 forward of the model per
+  candidate block set).  The dispatcher raises ``NotImplementedError`` for it.
+* The sparse branches need one-shot prefill, query length == key length, as
+  the reference's launchers assert (``q.shape == k.shape``); a query shorter
+  than the keys (a prefill continuing a cache) raises ``AssertionError``
+  instead of attending with unshifted positions.
 """
 
 from __future__ import annotations
 
-import itertools
 from dataclasses import dataclass
 
 import torch
@@ -172,6 +173,8 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
     """Run kernels 1, 2 and the router; return kv_idx plus the router state."""
     sel = SEL if sel is None else sel
     assert block_m == BLOCK, "selection tiles are 64 rows"
+    assert query.shape[-2] == key_states.shape[-2], (
+        "query length must equal key length (one-shot prefill: tile t sees blocks <= t)")
     assert query.is_cuda and query.dtype == torch.bfloat16, "bf16 HIP query required"
     assert key_states.dtype == torch.bfloat16 and key_states.device == query.device
     B, H, M, D = query.shape
@@ -394,181 +397,6 @@ def _block_select_mask(query, key_states, scaling, layer_idx):
     return keep
 
 
-def install_rollout_hooks(model):
-    """Keep each decoder layer's prefill input hidden state in ``SEL.hidden_at``
-    and the model in ``SEL.model_ref`` (src/sparse_attention.py:188-205); the
-    ``rollout_peek`` planner needs both."""
-    SEL.model_ref = model
-    SEL.hidden_at = {}
-
-    def capture(idx):
-        def hook(module, args, kwargs):
-            hs = args[0] if args else kwargs.get("hidden_states")
-            if hs is not None and hs.shape[-2] > 1:      # prefill only
-                SEL.hidden_at[idx] = hs.detach()
-            return None
-        return hook
-
-    for idx, layer in enumerate(model.model.layers):
-        layer.register_forward_pre_hook(capture(idx), with_kwargs=True)
-
-
-def _peek_score(hidden_post, layer_idx, position_embeddings, key_pool_t, last_pos):
-    """Score of one candidate: the next layer's block scores at the planning
-    row (src/sparse_attention.py:389-433).
-
-    Layer L's MLP and residual finish the row, layer L+1's input norm, q_proj
-    and RoPE form its query, which is scored against ``key_pool_t`` (the mean
-    K of each block, transposed and contiguous: [B, H_q, head_dim, NB]).  ``peakedness``: max minus median
-    of the head-mean scores; ``cross_head_agreement``: see
-    ``_peek_score_cross_head``.  0 without a model or a next layer.
-    """
-    if SEL.model_ref is None or position_embeddings is None:
-        return 0.0
-    layers = SEL.model_ref.model.layers
-    if layer_idx + 1 >= len(layers):
-        return 0.0
-    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
-    cur, nxt = layers[layer_idx], layers[layer_idx + 1]
-    hidden_next = hidden_post + cur.mlp(cur.post_attention_layernorm(hidden_post))
-    normed = nxt.input_layernorm(hidden_next)
-    n_heads = nxt.self_attn.config.num_attention_heads
-    hd = nxt.self_attn.head_dim
-    q_next = nxt.self_attn.q_proj(normed).view(1, 1, n_heads, hd).transpose(1, 2)
-    cos, sin = position_embeddings
-    q_next, _ = apply_rotary_pos_emb(q_next, q_next, cos[:, last_pos:last_pos + 1, :],
-                                     sin[:, last_pos:last_pos + 1, :])
-    scores = torch.matmul(q_next, key_pool_t) * nxt.self_attn.scaling
-    per_head = scores.squeeze(2).squeeze(0).float()                  # [H_q, NB]
-    if SEL.peek_metric == "peakedness":
-        bs = per_head.mean(dim=0)
-        return float((bs.max() - bs.median()).item())
-    if SEL.peek_metric == "cross_head_agreement":
-        return _peek_score_cross_head(per_head, SEL.budget_blocks)
-    raise ValueError(f"unknown peek_metric: {SEL.peek_metric}")
-
-
-def _peek_score_cross_head(per_head, budget):
-    """Number of blocks that at least ``SEL.peek_xh_threshold`` of the heads
-    put in their own top-``budget`` (src/sparse_attention.py:436-453)."""
-    n_heads, nb = per_head.shape
-    top = per_head.topk(min(budget, nb), dim=-1).indices
-    votes = torch.zeros(nb, device=per_head.device, dtype=torch.float32)
-    votes.scatter_add_(0, top.flatten(), torch.ones(top.numel(), device=per_head.device))
-    return float((votes >= SEL.peek_xh_threshold * n_heads).sum().item())
-
-
-def peek_plan(module, query, key_states, value_states, scaling, position_embeddings,
-              block_score, keep, layer_idx, trace=None):
-    """Override the planning rows of a baseline top-k ``keep`` with the best
-    candidate set of a depth-1 forward peek (src/sparse_attention.py:505-573).
-
-    block_score: [B, H, Q, NB] scores the baseline ranked (invisible blocks
-    -inf); keep: [B, H, Q, NB] bool, modified in place and returned.
-    key_states / value_states may carry H or Hk heads (GQA).  Planning rows
-    are the ``SEL.peek_rows_per_layer`` rows with the largest head-mean gap
-    between the first and the (budget+1)-th score among rows with at least
-    budget + peek_swap_w visible blocks; each keeps its budget - w best blocks
-    (head-mean order) and tries every way of filling the rest from the next
-    2w, scored one candidate at a time in enumeration order (the first best
-    wins).  Device-agnostic torch: the caller's tensors and the model's own
-    modules.  ``trace`` (a dict, optional) receives per planning row the
-    candidate block lists, their scores and the chosen list.
-    """
-    B, H, Q, D = query.shape
-    Hk, K = key_states.shape[1], key_states.shape[-2]
-    nb = (K + BLOCK - 1) // BLOCK
-    dev = query.device
-    q_global = torch.arange(K - Q, K, device=dev)
-    visible = (torch.arange(nb, device=dev) * BLOCK).view(1, nb) <= q_global.view(Q, 1)
-    block_score = block_score.masked_fill(~visible, float("-inf"))
-    bud = int(SEL.budget_blocks)
-    w = SEL.peek_swap_w
-    n_valid = visible.sum(dim=-1)
-    enumerable = n_valid >= bud + w
-    top_vals = torch.topk(block_score[0], k=min(bud + 1, nb), dim=-1).values
-    row_peak = (top_vals[..., 0] - top_vals[..., -1]).float().mean(dim=0)
-    row_peak = torch.where(enumerable, row_peak, torch.full_like(row_peak, -float("inf")))
-    n_plan = min(SEL.peek_rows_per_layer, int(enumerable.sum().item()))
-    hidden_full = SEL.hidden_at.get(layer_idx)
-    if (not SEL.peek_layer_min <= layer_idx <= SEL.peek_layer_max or n_plan == 0
-            or hidden_full is None or hidden_full.shape[-2] != K):
-        return keep
-    planning_rows = row_peak.argsort(descending=True)[:n_plan].tolist()
-    next_pool = SEL.k_pool_at.get(layer_idx + 1, SEL.k_pool_at.get(layer_idx))
-    # batched products take contiguous right operands (no transposed views)
-    pool_t = next_pool.transpose(-2, -1).contiguous() if next_pool is not None else None
-    k_t = key_states.transpose(2, 3).contiguous()
-    grp = H // Hk
-    keys = torch.arange(K, device=dev)
-    for r in planning_rows:
-        row_pos = int(q_global[r].item())
-        order = torch.argsort(block_score[0, :, r, :].mean(dim=0), descending=True).tolist()
-        n_v = int(n_valid[r].item())
-        bud_eff = min(bud, max(1, n_v))
-        safe_end = max(0, bud_eff - w)
-        safe = order[:safe_end]
-        band = order[safe_end:min(n_v, bud_eff + w)]
-        need = bud_eff - len(safe)
-        if need <= 0 or need > len(band):
-            continue
-        # the row's scores against every key (the same for every candidate)
-        q_row = query[:, :, r:r + 1, :].reshape(B, Hk, grp, D)
-        s_row = (torch.matmul(q_row, k_t) * scaling).reshape(B, H, 1, K)
-        hidden_row = hidden_full[:, r:r + 1, :]
-        causal = keys <= row_pos
-        best_score, best_blocks = -float("inf"), None
-        for combo in itertools.combinations(band, need):
-            blocks = safe + list(combo)
-            cand = torch.zeros(nb, dtype=torch.bool, device=dev)
-            cand[blocks] = True
-            ck = cand.repeat_interleave(BLOCK)[:K] & causal
-            a_row = F.softmax(s_row.masked_fill(~ck.view(1, 1, 1, K), float("-inf")),
-                              dim=-1, dtype=torch.float32).to(query.dtype)
-            attn = torch.matmul(a_row.reshape(B, Hk, grp, K), value_states)   # [B, Hk, grp, D]
-            o_proj_out = module.o_proj(attn.reshape(B, 1, H * D))
-            if SEL.peek_metric == "residual_norm":
-                score = float(o_proj_out.float().norm().item())
-            else:
-                score = _peek_score(hidden_row + o_proj_out, layer_idx, position_embeddings,
-                                    pool_t, row_pos)
-            if trace is not None:
-                trace.setdefault(r, {"candidates": [], "scores": []})
-                trace[r]["candidates"].append(blocks)
-                trace[r]["scores"].append(score)
-            if score > best_score:
-                best_score, best_blocks = score, blocks
-        if trace is not None and r in trace:
-            trace[r]["chosen"] = best_blocks
-        if best_blocks is not None:
-            row_keep = torch.zeros(nb, dtype=torch.bool, device=dev)
-            row_keep[best_blocks] = True
-            row_keep[0] = True                                    # sink
-            row_keep[row_pos // BLOCK] = True                     # own block
-            keep[0, :, r, :] = row_keep.unsqueeze(0).expand(H, nb)
-    return keep
-
-
-def _block_select_mask_peek(module, query, key_states, value_states, scaling,
-                            position_embeddings, trace=None):
-    """rollout_peek selection (src/sparse_attention.py:455-583): the v1 top-k
-    baseline on K-mean scores from the HIP selector, then ``peek_plan``
-    (``trace`` as there)."""
-    base = Selector()
-    base.__dict__.update({k: v for k, v in SEL.__dict__.items()
-                          if not isinstance(v, (list, dict))})
-    base.mode = "topk"
-    base.k_pool_at = SEL.k_pool_at                 # the K-mean pool is cached for the planner
-    res = select_mask_v1(query, key_states, scaling, sel=base, want_scores=True,
-                         layer_idx=module.layer_idx)
-    keep = peek_plan(module, query, key_states, value_states, scaling, position_embeddings,
-                     res.scores, res.keep, module.layer_idx, trace=trace)
-    if SEL.log:
-        SEL.kept_blocks[module.layer_idx] = keep[0, :, -1, :].any(dim=0).cpu()
-        SEL.budget_samples.append(keep[0, :, -1, :].sum(dim=-1).float().mean().item())
-    return keep
-
-
 def needle_hit_rate(needle_blocks) -> float:
     """Mean over logged layers of the fraction of ``needle_blocks`` kept for
     the last Q tile (union over heads), read from ``SEL.kept_blocks`` as the
@@ -590,7 +418,7 @@ def block_sparse_attention(module, query, key, value, attention_mask,
     query [B, H, S, D]; key / value [B, Hk, S, D] as transformers passes them
     (before repeat_kv).  Dense SDPA for ``mode == "dense"`` or decode (Q == 1);
     the HIP v2 path for topk / router / quest with ``SEL.kernel_v2``; the HIP
-    v1 per-row path otherwise (:790-804).  Returns
+    v1 per-row path otherwise (:790-804).  The sparse paths need S_q == S_k.  Returns
     ``(attn_output [B, S, H, D] contiguous, None)``.
     """
     Q = query.shape[-2]
@@ -604,6 +432,10 @@ def block_sparse_attention(module, query, key, value, attention_mask,
         PROF.stop(ev)
         return out.transpose(1, 2).contiguous(), None
 
+    # query row i is key position i in the selector's tile visibility and in
+    # the kernels' causal mask (one-shot prefill)
+    assert key.shape[-2] == Q, (
+        f"sparse prefill needs query length == key length (got {Q} vs {key.shape[-2]})")
     if SEL.kernel_v2 and SEL.mode in ("topk", "router", "quest"):
         ev = PROF.start("v2_select") if is_prefill else None
         kv_idx = _block_select_kv_idx_v2(query, key, scaling)   # resolved at call time
@@ -618,10 +450,11 @@ def block_sparse_attention(module, query, key, value, attention_mask,
         return out, None
 
     if SEL.mode == "rollout_peek":
-        keep = _block_select_mask_peek(module, query, key, value, scaling,
-                                       kwargs.get("position_embeddings"))
-    else:
-        keep = _block_select_mask(query, key, scaling, module.layer_idx)
+        raise NotImplementedError(
+            "SEL.mode 'rollout_peek' is not part of this build: it is an abandoned research "
+            "mode of the reference (a model-level planner off the sparse-prefill path); use "
+            "'topk', 'quest', 'router', 'belief' or 'rollout'")
+    keep = _block_select_mask(query, key, scaling, module.layer_idx)
     B, _, S, D = query.shape
     out = torch.empty(B, S, H, D, dtype=query.dtype, device=query.device)
     ws = attn_workspace(B, Hk, key.shape[-2], D, query.device)
