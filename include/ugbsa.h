@@ -139,6 +139,22 @@ int ugbsa_select_mask(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, i
                       int k_max, float top_p, const float* penalty, float* workspace,
                       int64_t workspace_elems, uint8_t* keep, float* margin, void* stream);
 
+/* ugbsa_select_mask without a caller workspace.  No counterpart in the
+ * reference: it serves callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Arguments and results as ugbsa_select_mask; the per-row scores of each pass
+ * go to a file-scope device array of 2^24 fp32 (64 MiB) per GPU, held until
+ * the process ends, instead of `workspace`.  Needs B * H * 64 * NB <= 2^24 (one
+ * 64-row tile per pass; larger shapes return UGBSA_EARG before any launch)
+ * and calls no allocator.  Every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU (other streams, other threads) race; the
+ * array keeps the last call's scores, and nothing in it needs clearing. */
+int ugbsa_select_mask_static(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                             int64_t sq_d, const void* planes, int B, int H, int Hk, int M, int N,
+                             int D, int dtype, int mode, float scaling, int policy, int k_bud,
+                             int k_eff, int k_min, int k_max, float top_p, const float* penalty,
+                             uint8_t* keep, float* margin, void* stream);
+
 /* v1 router (src/sparse_attention.py:317-354): margin_eff = margin, or its
  * head mean for row grain; rows with more than k_eff visible blocks are
  * eligible; quantile: thr = k_quant-th smallest of m_safe (margin_eff, +inf

@@ -78,6 +78,11 @@ def test_argument_errors_are_reported_without_launch(lib):
                             1, 8, 2, 64, 128, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
                             16, 0, 0, 8, 1, 16, None)
     assert rc == -1 and b"query length" in lib.ugbsa_last_error()
+    # the static-scratch selector refuses shapes whose one-tile pass exceeds its 2^24 fp32
+    rc = lib.ugbsa_select_mask_static(16, 0, 0, 8, 1, 16, 1, 128, 2, 4096 * 64, 4096 * 64, 128,
+                                      _capi.DTYPE_BF16, _capi.MODE_QUEST, 0.1, _capi.V1_TOPK, 4,
+                                      0, 1, 112, 0.9, None, 16, None, None)
+    assert rc == -1 and b"static scratch" in lib.ugbsa_last_error()
     # score dump: rho_k must stay below NB (the reference indexes s(rho_k))
     rc = lib.ugbsa_score_dump(16, 0, 0, 8, 1, 16, 1, 8, 2, 256, 256, 128, _capi.DTYPE_BF16,
                               _capi.MODE_QUEST, 0.1, 2, 4, 16, 16, 16, 16, 16, 16, None, None)

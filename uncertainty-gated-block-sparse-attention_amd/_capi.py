@@ -42,6 +42,8 @@ SIGNATURES = {
     "ugbsa_select_mask_workspace_elems": (_i64, [_i, _i, _i, _i]),
     "ugbsa_select_mask": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i, _i, _i,
                                _f, _i, _i, _i, _i, _i, _f, _p, _p, _i64, _p, _p, _p]),
+    "ugbsa_select_mask_static": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i, _i, _i, _i, _i, _i,
+                                      _i, _i, _f, _i, _i, _i, _i, _i, _f, _p, _p, _p, _p]),
     "ugbsa_router_rows": (_i, [_p, _i, _i, _i, _i, _i, _i, _f, _i64, _i, _p, _p, _p, _p, _p]),
     "ugbsa_keep_kv_idx": (_i, [_p, _i, _i, _i, _i, _i, _p, _p, _p, _p]),
     "ugbsa_attn_fwd_rows": (_i, [_p, _i64, _i64, _i64, _i64,

@@ -3,6 +3,7 @@
 // interfaces each entry point replaces: include/ugbsa.h.
 #include <cstdio>
 #include <cstdarg>
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -205,6 +206,36 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
 
 namespace {
 
+// ---- static scratch of ugbsa_select_mask_static ---------------------------
+// The per-row scores of the v1 selector's passes live in this file-scope
+// array instead of a caller workspace: kStaticScratchFloats fp32 (64 MiB) on
+// every device the library runs on, held until the process ends.  Host code
+// must not pass the array's name to a kernel (it is a host-side stand-in);
+// its device address is looked up once per device, with that device current,
+// and kept in g_scratch_ptr.
+constexpr int64_t kStaticScratchFloats = int64_t(1) << 24;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) float scratch[kStaticScratchFloats];
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+int static_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_result(e, "select_mask_static: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(UGBSA_EARG, "device %d beyond the %d the static scratch tracks", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_result(e, "select_mask_static: hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(UGBSA_EARG, "select_mask_static: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<float*>(g_scratch_ptr[dev]);
+  return UGBSA_OK;
+}
+
 int select_mask_impl(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
                       const void* planes, int B, int H, int Hk, int M, int N, int D, int dtype,
                       int mode, float scaling, int policy, int k_bud, int k_eff, int k_min,
@@ -234,7 +265,16 @@ int select_mask_impl(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, in
   if (K > ugbsa::kMaxSlots) return fail(UGBSA_EARG, "ranking %d blocks deep exceeds %d", K, ugbsa::kMaxSlots);
   const int64_t per_row = static_cast<int64_t>(B) * H * nb;
   const int64_t chunk_tiles = workspace_elems / (per_row * ugbsa::kBlock);
-  if (chunk_tiles < 1) return fail(UGBSA_EARG, "workspace of %lld floats holds less than one 64-row tile (%lld)", (long long)workspace_elems, (long long)(per_row * ugbsa::kBlock));
+  if (chunk_tiles < 1) {
+    if (workspace == nullptr)
+      return fail(UGBSA_EARG, "select_mask_static: one 64-row tile needs B*H*64*NB = %lld fp32, beyond the %lld of the static scratch",
+                  (long long)(per_row * ugbsa::kBlock), (long long)workspace_elems);
+    return fail(UGBSA_EARG, "workspace of %lld floats holds less than one 64-row tile (%lld)", (long long)workspace_elems, (long long)(per_row * ugbsa::kBlock));
+  }
+  if (workspace == nullptr) {   // the static scratch of this device (sizes checked above)
+    rc = static_scratch(&workspace);
+    if (rc) return rc;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int Qt = (M + ugbsa::kBlock - 1) / ugbsa::kBlock;
   for (int t0 = 0; t0 < Qt; t0 += static_cast<int>(chunk_tiles)) {
@@ -373,6 +413,16 @@ int ugbsa_select_mask(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, i
   return select_mask_impl(q, sq_b, sq_h, sq_m, sq_d, planes, B, H, Hk, M, N, D, dtype, mode,
                           scaling, policy, k_bud, k_eff, k_min, k_max, top_p, penalty, workspace,
                           workspace_elems, keep, margin, stream);
+}
+
+int ugbsa_select_mask_static(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                             int64_t sq_d, const void* planes, int B, int H, int Hk, int M, int N,
+                             int D, int dtype, int mode, float scaling, int policy, int k_bud,
+                             int k_eff, int k_min, int k_max, float top_p, const float* penalty,
+                             uint8_t* keep, float* margin, void* stream) {
+  return select_mask_impl(q, sq_b, sq_h, sq_m, sq_d, planes, B, H, Hk, M, N, D, dtype, mode,
+                          scaling, policy, k_bud, k_eff, k_min, k_max, top_p, penalty, nullptr,
+                          kStaticScratchFloats, keep, margin, stream);
 }
 
 int ugbsa_router_rows(const float* margin, int B, int H, int M, int NB, int grain, int rmode,
