@@ -62,6 +62,10 @@ def parse_args():
     p.add_argument("--path", choices=("v2", "v1"), default="v2",
                    help="v2: per-tile selection (the headline); v1: the per-row path "
                         "(kernel_v2=False: per-row keep mask, keep-masked attention)")
+    p.add_argument("--list-overlap", action="store_true",
+                   help="print how much the emitted kv_idx lists share: visited (tile, block) "
+                        "slots against distinct (KV head, block) pairs over a KV group's heads "
+                        "and windows of consecutive tiles (one layer, no timing)")
     p.add_argument("--pmc-run", action="store_true",
                    help="untimed driver for rocprofv3 --pmc: --steps layers of the workload, "
                         "then two copies of a 1 GiB tensor (counter calibration)")
@@ -381,6 +385,34 @@ def pmc_run(cfg, steps, torch, synth, dev):
     print("pmc run done", flush=True)
 
 
+def list_overlap(runner, torch):
+    """Visited slots of the layer's kv_idx (block < NB and <= t) against the
+    number of distinct (b, KV head, window, block) tuples over the KV group's
+    query heads and windows of w consecutive tiles: how many of the visits a
+    cache that kept every block for one window would serve."""
+    runner.step()
+    torch.cuda.synchronize()
+    kv = runner.kv_idx.long()
+    B, H, Qt, _ = kv.shape
+    NB, Hk = runner.NB, runner.Hk
+    grp = H // Hk
+    t = torch.arange(Qt, device=kv.device).view(1, 1, Qt, 1)
+    ok = (kv >= 0) & (kv < NB) & (kv <= t)
+    res = {"visits": int(ok.sum())}
+    for w in (1, 2, 4, 8, 16):
+        seen = torch.zeros(B * Hk * ((Qt + w - 1) // w) * NB, dtype=torch.bool, device=kv.device)
+        win = (torch.arange(Qt, device=kv.device) // w).view(1, Qt, 1)
+        nwin = (Qt + w - 1) // w
+        for h in range(H):
+            g = h // grp
+            bidx = torch.arange(B, device=kv.device).view(B, 1, 1)
+            key = ((bidx * Hk + g) * nwin + win) * NB + kv[:, h].clamp(0, NB - 1)
+            seen[key[ok[:, h]]] = True
+        res[f"union_w{w}"] = int(seen.sum())
+        res[f"visits_per_union_w{w}"] = round(res["visits"] / max(1, res[f"union_w{w}"]), 2)
+    return res
+
+
 def run_v1(args, cfg, q, k, v, torch):
     """The v1 per-row path on one layer (SEL.kernel_v2 = False,
     src/sparse_attention.py:790-804): per-row selection + router
@@ -466,6 +498,10 @@ def main():
     if args.policy is not None:
         fields.update(POLICIES[args.policy])
     runner = LayerRunner(cfg, q, k, v, sel_fields=fields)
+    if args.list_overlap:
+        print(json.dumps({"config": cfg.name, "policy": policy_name(runner.sel),
+                          **list_overlap(runner, torch)}), flush=True)
+        return
     ms_step, per = run_layer_bench(runner, args.steps, args.warmup, torch)
     attn_flops = runner.attended_flops()
     exact_flops = runner.attended_flops(exact=True)
