@@ -357,7 +357,12 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   // pieces a thread prefetches into registers (enough for 4 or more waves;
   // smaller workgroups copy the rest when the chunk is stored)
   constexpr int STAGE = (PIECES + 255) / 256;
-  constexpr int QSETS = P == 2 ? 2 : 1;             // Quest: max(q, 0) and min(q, 0)
+  // Quest multiplies max(q, 0) by the K-max plane and min(q, 0) by the
+  // K-min plane.  The two signed copies of the Q tile are kept when they fit
+  // (2 * 4 * KS fragments); at head_dim 256, and in the streaming rows that
+  // hold extra state, only q is kept and the halves are formed per chunk.
+  constexpr bool SPLIT_LATE = P == 2 && (D > 128 || STREAM);
+  constexpr int QSETS = P == 2 && !SPLIT_LATE ? 2 : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   const SelectLds L = select_lds(P, D, NB, KP, CH, STREAM);
 
@@ -411,9 +416,9 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       for (int ks = 0; ks < KS; ++ks) {
         const bf16x8 x = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
                                              : zero_bf16x8();
-        if constexpr (P == 2) {
+        if constexpr (P == 2 && !SPLIT_LATE) {
           qf[0][mt][ks] = bf16_pos(x);
-          qf[QSETS - 1][mt][ks] = bf16_neg(x);
+          qf[1][mt][ks] = bf16_neg(x);
         } else {
           qf[0][mt][ks] = x;
         }
@@ -477,7 +482,16 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
                                                        p * D + 32 * ks + 8 * g4);
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt) {
-            const bf16x8 a = qf[P == 2 ? p : 0][mt][ks];
+            bf16x8 a;
+            if constexpr (SPLIT_LATE) {
+              // the opaque copy keeps the split inside the chunk loop (hoisted,
+              // both halves would stay live for the whole row)
+              bf16x8 x = qf[0][mt][ks];
+              asm volatile("" : "+v"(x));
+              a = p == 0 ? bf16_pos(x) : bf16_neg(x);
+            } else {
+              a = qf[P == 2 ? p : 0][mt][ks];
+            }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma16x16x32(a, bfr[nt], acc[mt][nt]);
           }
