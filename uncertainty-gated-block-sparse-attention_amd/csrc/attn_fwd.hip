@@ -133,26 +133,33 @@ __global__ __launch_bounds__(256) void kv_operand_kernel(
 
 // Work of each (b, t) tile of 64 query rows: the visited slots of its
 // kv_idx rows summed over the H query heads (slot values in [0, NB) and at
-// most t, the blocks the attention loop visits).  One wavefront per tile.
+// most t, the blocks the attention loop visits).  One workgroup per tile:
+// its four wavefronts take every fourth head, each lane every 64th slot, with
+// the loads of four slots in flight at once; the partial counts meet in LDS.
 __global__ __launch_bounds__(256) void tile_work_kernel(const int32_t* __restrict__ kv_idx,
                                                         int64_t si_b, int64_t si_h, int64_t si_t,
                                                         int B, int H, int Qt, int k_slots, int NB,
                                                         int32_t* __restrict__ work) {
-  const int lane = threadIdx.x & 63;
-  const int bt = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (bt >= B * Qt) return;
+  __shared__ int part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int bt = blockIdx.x;
   const int b = bt / Qt, t = bt - b * Qt;
   int cnt = 0;
-  for (int h = 0; h < H; ++h) {
+  for (int h = wave; h < H; h += 4) {
     const int32_t* row = kv_idx + b * si_b + h * si_h + t * si_t;
-    for (int s = lane; s < k_slots; s += 64) {
-      const int v = row[s];
-      cnt += (v >= 0 && v < NB && v <= t) ? 1 : 0;
+    for (int s0 = lane; s0 < k_slots; s0 += 256) {
+      int v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = s0 + 64 * j < k_slots ? row[s0 + 64 * j] : -1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cnt += (v[j] >= 0 && v[j] < NB && v[j] <= t) ? 1 : 0;
     }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
-  if (lane == 0) work[bt] = cnt;
+  if (lane == 0) part[wave] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) work[bt] = part[0] + part[1] + part[2] + part[3];
 }
 
 // The (b, t) tiles ordered by work, heaviest first: a stable counting sort
@@ -220,8 +227,7 @@ hipError_t launch_attn_tile_order(const int32_t* kv_idx, int64_t si_b, int64_t s
                                   int64_t si_t, int B, int H, int Qt, int k_slots, int NB,
                                   int32_t* ws, hipStream_t stream) {
   const int n = B * Qt;
-  tile_work_kernel<<<(n + 3) / 4, 256, 0, stream>>>(kv_idx, si_b, si_h, si_t, B, H, Qt, k_slots,
-                                                    NB, ws);
+  tile_work_kernel<<<n, 256, 0, stream>>>(kv_idx, si_b, si_h, si_t, B, H, Qt, k_slots, NB, ws);
   tile_order_kernel<<<1, kOrderThreads, 0, stream>>>(ws, B, Qt, ws + n);
   return hipGetLastError();
 }
