@@ -13,6 +13,11 @@ the way that holds at any size, and on samples where a full check does not fit:
 * kernel 2's own fp32 tile scores of two sampled heads, all tiles: the
   oracle's top-k of those rows reproduces the kernel's base slots exactly,
   and (router) its sigma margins bit for bit;
+* the same on every head and tile, with a stable descending torch.sort of
+  the kernel's scores on the GPU as the independent ranking (ties and the
+  -inf tail in ascending block order, as the contract's total order): base
+  and extra slots equal slot for slot, and sigma recomputed from the sorted
+  values in IEEE fp32 on the host equal bit for bit;
 * the router on the kernel's sigma of every head: the head mean, the
   k_quant-th smallest threshold and the trigger flags recomputed on the host
   bit for bit; sentinel NB exactly on the untriggered tiles, and the oracle's
@@ -122,6 +127,19 @@ def test_full_config_layer(hip_lib, layers, name, policy):
         assert ((extra == nb).all(axis=-1) == ~unc).all()
         for j, h in enumerate(heads):
             assert np.array_equal(extra[h][unc[h]], idx[0, j][unc[h]][:, k_base:])
+
+    # every head and tile: the kernel's ranking against a stable sort of its
+    # own scores (an implementation independent of the kernel's radix select)
+    T_all = res.tile_score[0]                                      # [H, Qt, NB] on the GPU
+    srt_v, srt_i = torch.sort(T_all, dim=-1, descending=True, stable=True)
+    kv_dev = res.kv_idx[0]
+    assert torch.equal(kv_dev[..., :k_base], srt_i[..., :k_base].int())
+    if router:
+        unc_dev = res.uncertain[0].bool()
+        assert torch.equal(kv_dev[..., k_base:][unc_dev], srt_i[..., k_base:k_slots][unc_dev].int())
+        vals_all = srt_v[..., :k_base + 1].cpu().numpy()[None]   # [1, H, Qt, k_base + 1]
+        assert same_float_bits(res.sigma.cpu().numpy(), OS.sigma_margin(vals_all, k_base))
+    del T_all, srt_v, srt_i
 
     # sampled tiles: independent oracle scores, selection from scratch, attention
     rng = np.random.default_rng(cfg.index)

@@ -28,7 +28,7 @@ import synth
 from block_attn import attn_workspace, block_sparse_attn_v2
 from oracle import attention as OA
 from oracle import selector as OS
-from parity import score_gap_tol, unexplained_differences
+from parity import same_float_bits, score_gap_tol, unexplained_differences
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -83,6 +83,18 @@ def test_long_context_select_and_attention(hip_lib, S):
     trig = unc[:, k_slots:]
     ex = extra[:, k_slots:][trig]
     assert (ex < nb).all() and (np.diff(np.sort(ex, axis=-1), axis=-1) > 0).all()
+
+    # three heads, every tile: the kernel's ranking against a stable sort of its
+    # own scores on the GPU (ties and the -inf tail in ascending block order)
+    for h in (0, 13, 27):
+        srt_v, srt_i = torch.sort(res.tile_score[0, h], dim=-1, descending=True, stable=True)
+        assert torch.equal(res.kv_idx[0, h, :, :k_base], srt_i[:, :k_base].int()), h
+        trig_h = res.uncertain[0, h].bool()
+        assert torch.equal(res.kv_idx[0, h, :, k_base:][trig_h], srt_i[:, k_base:k_slots][trig_h].int())
+        vals_h = srt_v[:, :k_base + 1].cpu().numpy()[None, None]
+        assert same_float_bits(res.sigma[0, h].cpu().numpy()[None, None],
+                               OS.sigma_margin(vals_h, k_base)), h
+        del srt_v, srt_i
 
     # router decisions recomputed on the host from the kernel's sigma
     sig = res.sigma.cpu().numpy()

@@ -188,6 +188,15 @@ def test_select_c2_full_config(hip_lib):
     T_k = res.tile_score[:, :7].cpu().numpy()
     fin = np.isfinite(T_or)
     assert np.abs(T_or[fin] - T_k[fin]).max() <= 1e-5
+    # every head and tile: the kernel's ranking against a stable sort of its
+    # own scores on the GPU (ties and the -inf tail in ascending block order)
+    srt_v, srt_i = torch.sort(res.tile_score[0].to(DEV), dim=-1, descending=True, stable=True)
+    kv_dev = res.kv_idx[0]
+    assert torch.equal(kv_dev[..., :res.k_base], srt_i[..., :res.k_base].int())
+    unc_dev = res.uncertain[0].bool()
+    assert torch.equal(kv_dev[..., res.k_base:][unc_dev],
+                       srt_i[..., res.k_base:res.k_slots][unc_dev].int())
+    del srt_v, srt_i
     # from-scratch selection of those heads under the kernel's trigger flags
     k_base, k_slots = res.k_base, res.k_slots
     _, idx_or = OS.topk_order(T_or, k_slots)
