@@ -353,7 +353,7 @@ def attention_kernel_label(D, NB):
     runs for 64-row tiles (csrc/attn_fwd.hip)."""
     if D == 256:
         return "attn_fwd_pipe_kernel<256, 2, true, true>"
-    return f"attn_fwd_pipe_kernel<{D}, 4, false, {'true' if D == 128 and NB > 1024 else 'false'}>"
+    return f"attn_fwd_pipe_kernel<{D}, 4, false, false>"
 
 
 def roofline(cfg_name, D, NB, tflops):

@@ -169,20 +169,6 @@ def test_strided_views_and_repeat_kv_heads(hip_lib):
     assert torch.equal(rep, base)
 
 
-@pytest.mark.parametrize("variant", ["1", "0"])
-def test_d128_prefetch_variants(hip_lib, monkeypatch, variant):
-    """Both head_dim-128 variants of the pipelined kernel on the small cases:
-    one K / V^T register set requested a phase ahead (chosen above 1024
-    context blocks) and two sets requested two half blocks ahead, forced
-    through UGBSA_PIPE_LONG."""
-    print(f"[case] d128 prefetch variant UGBSA_PIPE_LONG={variant}", flush=True)
-    monkeypatch.setenv("UGBSA_PIPE_LONG", variant)
-    test_sparse_gqa_ragged(hip_lib, 128, 64)
-    test_score_drift_and_negative_scale(hip_lib, 128, 64)
-    test_repeated_slot_counts_twice(hip_lib)
-    test_strided_views_and_repeat_kv_heads(hip_lib)
-
-
 class _Module:
     num_key_value_groups = 7
     layer_idx = 0

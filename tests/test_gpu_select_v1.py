@@ -267,13 +267,6 @@ def test_v1_attention_over_keep(hip_lib, D, Hq, Hk, bm):
     assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
 
 
-def test_v1_attention_over_keep_long_variant(hip_lib, monkeypatch):
-    """Row-masked attention through the head_dim-128 variant used above 1024
-    context blocks (one K / V^T set a phase ahead), forced on a small case."""
-    monkeypatch.setenv("UGBSA_PIPE_LONG", "1")
-    test_v1_attention_over_keep(hip_lib, 128, 4, 1, 64)
-
-
 class _Module:
     num_key_value_groups, layer_idx = 4, 0
 

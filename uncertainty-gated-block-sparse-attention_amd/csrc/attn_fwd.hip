@@ -35,7 +35,6 @@
 // i runs on XCD i % 8), so their shared picks (sink, local, group needles)
 // hit the same L2; long contexts launch the units in generations
 // (attn_pipe.h, launch_attn_pipe).
-#include <cstdlib>
 
 #include "common.h"
 #include "launch.h"
@@ -534,14 +533,6 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
       return launch_attn_pipe256(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b,
                                  si_h, si_t, B, H, Hk, M, N, Qt, k_slots, scale, out, so_b, so_h,
                                  so_m, stream, tile_order);
-    // the single-set prefetch above kPipeLongBlocks context blocks;
-    // UGBSA_PIPE_LONG=0/1 forces either variant (tests)
-    const char* lv = getenv("UGBSA_PIPE_LONG");
-    const bool long_ctx = lv != nullptr ? lv[0] == '1' : (N + kBlock - 1) / kBlock > kPipeLongBlocks;
-    if (D == 128 && long_ctx)
-      return launch_attn_pipe128_long(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
-                                      rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
-                                      scale, out, so_b, so_h, so_m, stream, tile_order);
     if (D == 128)
       return launch_attn_pipe<128, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                           rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,

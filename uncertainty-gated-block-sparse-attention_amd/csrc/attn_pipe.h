@@ -1,7 +1,7 @@
 // The software-pipelined attention kernel over per-tile kv_idx (64-row
-// tiles), shared by the head_dim 64 / 128 builds (attn_fwd.hip and, for long
-// contexts, attn_fwd_long.hip; one wavefront per tile) and the head_dim 256
-// build (attn_fwd256.hip, two wavefronts of 32 rows per tile).
+// tiles), shared by the head_dim 64 / 128 builds (attn_fwd.hip, one
+// wavefront per tile) and the head_dim 256 build (attn_fwd256.hip, two
+// wavefronts of 32 rows per tile).
 #pragma once
 
 #include "common.h"
@@ -25,8 +25,8 @@ namespace ugbsa {
 // register sets alternate between consecutive steps (the loop is unrolled by
 // 2).  Half blocks keep the live set at about 470 registers: O^T 128, two S
 // 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K 64, two V^T 64.
-// With SB (head_dim 256, and head_dim 128 for long contexts) K / V^T keep
-// one set each, requested one phase ahead, and phase 1 computes all of P(u)
+// With SB (head_dim 256) K / V^T keep one set each, requested one phase
+// ahead, and phase 1 computes all of P(u)
 // while phase 2 forms the lane maxima of S(u+1) and tests them against the
 // lazy threshold (the rescale follows phase 2 when one moved).  Head_dim 256
 // (QLDS) doubles O^T, K and V^T, so Q moves to LDS.
@@ -502,11 +502,10 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
 
   SBuf sa, sb;
   if constexpr (SB) {
-    // One K and one V^T set (at head_dim 256 two would take 256 registers;
-    // at head_dim 128 the single set keeps fewer bytes in flight).
+    // One K and one V^T set (at head_dim 256 two would take 256 registers).
     // Step u: S(u) in cur, K(u+1) in ka, V(u) in va; K(u+2) is requested
     // after phase 1 and V(u+1) after phase 2 — a phase ahead of use (about
-    // 2000 cycles at head_dim 256, 1000 at 128).
+    // 2000 cycles at head_dim 256).
     auto step1 = [&](SBuf& cur, SBuf& nxt, int u) {
       const int rk = blk_raw(u + 2), rm1 = blk_raw(u + 1);
       phase1(cur, nxt, ka);
@@ -631,13 +630,14 @@ static int resident_workgroups(Kern kern, int threads, size_t lds) {
 // ascending block lists in step, so a block that several tiles of a KV head
 // list (the group's heads and the tiles around it pick many of the same
 // blocks) is fetched into the XCD's L2 once for all of them.  Measured on
-// MI355X, attention launch ms, one launch / generations of 1x / 2x / 3x the
-// resident workgroups: c3 (128K, head_dim 128) 21.8 / 18.7 / 18.5 / 18.5,
-// 64K 9.4 / 9.6 / 9.5 / 9.3, c5 (128K, head_dim 256) 37.7 / 27.6 / 28.2 /
-// 29.1; at 32K (512 blocks, where L2 already holds 89 % of the re-reads) one
-// launch, 2.13 against 2.30 / 2.23 / 2.20.  The fabric traffic of the c3
-// launch falls from 120 GB to 19 GB.  A fractional multiple leaves a partial
-// last wave in every launch (x1.5: 22.4 ms at c3).
+// MI355X, attention launch ms, one launch / generations of 1x / 2x / 3x / 4x
+// the resident workgroups: c3 (128K, head_dim 128) 21.8 / 17.8 / 17.6 / 17.6
+// / 17.5, 64K 9.4 / 9.4 / 9.5 / 9.2-9.3 / 9.2, c5 (128K, head_dim 256) 37.7
+// / 27.6 / 28.2 / 29.1 / 29.8; at 32K (512 blocks, where L2 already holds
+// 89 % of the re-reads) one launch, 2.13 against 2.30 / 2.23 / 2.20 / 2.19.
+// The fabric traffic of the c3 launch falls from 120 GB to about 20 GB.  A
+// fractional multiple leaves a partial last wave in every launch (x1.5:
+// 22.4 ms at c3).
 constexpr int kGenBlocks = 512;
 template <int D>
 constexpr int gen_waves() { return D > 128 ? 1 : 3; }

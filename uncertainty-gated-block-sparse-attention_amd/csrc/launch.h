@@ -124,19 +124,6 @@ hipError_t launch_attn_pipe256(const uint16_t* q, int64_t sq_b, int64_t sq_h, in
                                int64_t so_h, int64_t so_m, hipStream_t stream,
                                const int32_t* tile_order);
 
-// The pipelined attention kernel at head_dim 128 with one K / V^T set
-// requested a phase ahead (attn_fwd_long.hip), for contexts of more than
-// kPipeLongBlocks blocks.
-constexpr int kPipeLongBlocks = 1024;
-hipError_t launch_attn_pipe128_long(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
-                                    const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                                    const uint16_t* vt, const int32_t* kv_idx,
-                                    const uint64_t* rowmask, int64_t si_b, int64_t si_h,
-                                    int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
-                                    int k_slots, float scale, uint16_t* out, int64_t so_b,
-                                    int64_t so_h, int64_t so_m, hipStream_t stream,
-                                    const int32_t* tile_order);
-
 // _compute_kv_idx on the GPU: per (b, h, block_m-row tile) the blocks any row
 // of keep [B, H, M, NB] (uint8, contiguous) keeps, ascending, NB-padded to
 // NB slots, their count, and (if rowmask) each listed block's row mask.
