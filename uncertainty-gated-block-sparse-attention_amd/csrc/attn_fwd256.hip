@@ -1,7 +1,8 @@
-// Kernel 3 at head_dim 256: the pipelined attention kernel (attn_pipe.h)
-// with a 64-row tile split over two wavefronts of 32 rows (a 64-row O^T
-// alone would take 256 registers), Q staged in LDS and one K / V^T register
-// set per wave.
+// Kernel 3 at head_dim 256: the pipelined attention kernel (attn_pipe.h),
+// one wavefront per 64-row tile, with the tile's O^T (256 registers) in the
+// AGPR file, accumulated there by the P.V MFMAs; Q staged in LDS, one K / V^T
+// register set.  (Two 32-row wavefronts per tile, each holding half of O^T
+// in VGPRs, fetch every K / V^T block twice: 6-7 % slower at c5.)
 #include "attn_pipe.h"
 
 namespace ugbsa {
@@ -14,7 +15,7 @@ hipError_t launch_attn_pipe256(const uint16_t* q, int64_t sq_b, int64_t sq_h, in
                                int k_slots, float scale, uint16_t* out, int64_t so_b,
                                int64_t so_h, int64_t so_m, hipStream_t stream,
                                const int32_t* tile_order) {
-  return launch_attn_pipe<256, 2, true, true>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
+  return launch_attn_pipe<256, 4, true, true, true>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                            rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt,
                                            k_slots, scale, out, so_b, so_h, so_m, stream, tile_order);
 }

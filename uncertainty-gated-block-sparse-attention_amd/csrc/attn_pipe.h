@@ -1,7 +1,6 @@
 // The software-pipelined attention kernel over per-tile kv_idx (64-row
-// tiles), shared by the head_dim 64 / 128 builds (attn_fwd.hip, one
-// wavefront per tile) and the head_dim 256 build (attn_fwd256.hip, two
-// wavefronts of 32 rows per tile).
+// tiles, one wavefront per tile), shared by the head_dim 64 / 128 builds
+// (attn_fwd.hip) and the head_dim 256 build (attn_fwd256.hip, O^T in AGPRs).
 #pragma once
 
 #include "common.h"
@@ -25,11 +24,13 @@ namespace ugbsa {
 // register sets alternate between consecutive steps (the loop is unrolled by
 // 2).  Half blocks keep the live set at about 470 registers: O^T 128, two S
 // 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K 64, two V^T 64.
-// With SB (head_dim 256) K / V^T keep one set each, requested one phase
-// ahead, and phase 1 computes all of P(u)
-// while phase 2 forms the lane maxima of S(u+1) and tests them against the
-// lazy threshold (the rescale follows phase 2 when one moved).  Head_dim 256
-// (QLDS) doubles O^T, K and V^T, so Q moves to LDS.
+// With SB (head_dim 256) K / V^T keep one set each: K requested after
+// phase 1 (a phase ahead of use), each V^T fragment right after the P.V
+// MFMAs that read it; phase 1 computes all of P(u) while phase 2 forms the
+// lane maxima of S(u+1) and tests them against the lazy threshold (the
+// rescale follows phase 2 when one moved).  Head_dim 256 (QLDS) doubles
+// O^T, K and V^T, so Q moves to LDS and O^T (256 registers for 64 rows) to
+// the AGPR file (OA), where only the P.V MFMAs touch it.
 // The tile's kv_idx row is compacted into LDS once (visited blocks only), so
 // sentinel and invisible slots cost nothing in the loop.
 // Per-wave LDS bytes of attn_fwd_pipe_kernel: Q fragments (QLDS), block
@@ -42,7 +43,7 @@ __host__ __device__ inline int pipe_wave_lds(int D, int NT, bool qlds, int k_slo
   return (bytes + 15) / 16 * 16;
 }
 
-template <int D, int NT, bool QLDS, bool SB>
+template <int D, int NT, bool QLDS, bool SB, bool OA>
 __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
@@ -55,6 +56,9 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // NT = 4: one wavefront per 64-row tile; NT = 2: two wavefronts, 32 rows
   // each, which run independently (each keeps its own copy of the list)
   static_assert(NT == 4 || NT == 2, "a wavefront takes 64 or 32 rows of a tile");
+  // OA: O^T accumulates in AGPRs (a 64-row tile at head_dim 256 fills all
+  // 256 of them), written only by the P.V MFMAs of the SB loop
+  static_assert(!OA || SB, "AGPR accumulators are used by the single-set loop");
   const int wave = threadIdx.x >> 6;
   // dynamic LDS per wave: [Q fragments (QLDS)] [block list] [bitmap] [row masks]
   extern __shared__ __align__(16) unsigned char psm_all[];
@@ -122,17 +126,29 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // Global (not buffer) loads: a wavefront streams K/V through the vector
   // memory pipeline faster with them, and every visited block lies inside
   // the operand copy, so no range check is needed.
+  // First K / V^T slab of half block (blk, half), a wave-uniform address
+  // (with blk uniform), and slab s of it for this lane: a scalar base plus a
+  // 32-bit lane offset, so the loads take the SGPR-base form and no 64-bit
+  // address per lane stays live in VGPRs.
+  auto k_ptr = [&](int blk, int half) -> gchar* {
+    return (gchar*)(kop_head) + static_cast<int64_t>(2 * blk + half) * (2 * KS * 1024);
+  };
+  auto v_ptr = [&](int blk, int half) -> gchar* {
+    return (gchar*)(vop_head) + static_cast<int64_t>(2 * blk + half) * (DT * 1024);
+  };
+  uint32_t lane_b = static_cast<uint32_t>(lane) * 16u;
+  auto slab = [&](gchar* base, int s) -> bf16x8 { return load_slab(base, lane_b, s); };
   auto load_k = [&](int blk, int half, KSet& kf) {
-    const uint16_t* p = kop_head + static_cast<int64_t>(2 * blk + half) * (2 * KS * 512) + lane * 8;
+    gchar* p = k_ptr(blk, half);
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = load_bf16x8(p + (mt * KS + ks) * 512);
+      for (int ks = 0; ks < KS; ++ks) kf[mt][ks] = slab(p, mt * KS + ks);
   };
   auto load_v = [&](int blk, int half, VSet& vf) {
-    const uint16_t* p = vop_head + static_cast<int64_t>(2 * blk + half) * (DT * 512) + lane * 8;
+    gchar* p = v_ptr(blk, half);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) vf[dt] = load_bf16x8(p + dt * 512);
+    for (int dt = 0; dt < DT; ++dt) vf[dt] = slab(p, dt);
   };
   // The first operands are requested before the list is known, for block 0:
   // the visited blocks are ascending and the selector forces the sink block
@@ -258,7 +274,10 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NT; ++nt) {
+      o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (OA) asm volatile("" : "+a"(o[dt][nt]));
+    }
   float m[NT], l[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) { m[nt] = -1e30f; l[nt] = 0.f; }
@@ -340,7 +359,18 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   };
   // Move the offsets to the new row maxima (lane maxima rm -> row maxima)
   // and rescale l and O.
+  // With OA, every VALU access to O^T waits for the P.V MFMAs to retire.
+  auto drain_o = [&]() {
+    if constexpr (OA) {
+      agpr_drain();
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+a"(o[dt][nt]));
+    }
+  };
   auto rescale = [&]() {
+    drain_o();
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const float m_new = fmaxf(m[nt], quad_rows_max(rm[nt]) * sl2);
@@ -349,7 +379,12 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       thr[nt] = (m_new + kLazyLog2) * inv_sl2;
       l[nt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= alpha;
+      for (int dt = 0; dt < DT; ++dt) {
+        o[dt][nt] *= alpha;
+        // back into its AGPRs at once: left to the allocator, all 256
+        // products would stay in VGPRs until the next MFMA reads them
+        if constexpr (OA) asm volatile("" : "+a"(o[dt][nt]));
+      }
     }
   };
   // Softmax element e of S (nt = e / 8): P = exp2(S * sl2 - m), the row sum
@@ -395,14 +430,22 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   auto phase1 = [&](const SBuf& cur, SBuf& nxt, const KSet& kf) {
     if constexpr (QLDS) {
       // pair j = (ks, nt): both M-tiles of fragment (nt, ks); the fragment
-      // of pair j + 2 is requested in pair j, two MFMA pairs ahead of use
+      // of pair j + 2 is requested in pair j, two MFMA pairs ahead of use.
+      // Pairs run over the row sets two at a time (ks inside), so S(u+1)
+      // comes into being two row sets at a time while the softmax of S(u)
+      // frees its row sets in order: with OA that keeps the two S sets
+      // within 48 live registers instead of 64.  Four accumulators cycle,
+      // so a dependent MFMA issues 64 cycles after its predecessor.
+      constexpr int NTG = NT >= 2 ? 2 : NT;         // row sets per group
+      auto pair_nt = [](int j) { return (j / (NTG * KS)) * NTG + j % NTG; };
+      auto pair_ks = [](int j) { return (j % (NTG * KS)) / NTG; };
       bf16x8 qr[3];
-      qr[0] = qfrag(0, 0);
-      qr[1] = qfrag(1 % NT, 1 / NT);
+      qr[0] = qfrag(pair_nt(0), pair_ks(0));
+      qr[1] = qfrag(pair_nt(1), pair_ks(1));
       static_for<P1>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        constexpr int ks = j / NT, nt = j % NT;
-        if constexpr (j + 2 < P1) qr[(j + 2) % 3] = qfrag((j + 2) % NT, (j + 2) / NT);
+        constexpr int ks = pair_ks(j), nt = pair_nt(j);
+        if constexpr (j + 2 < P1) qr[(j + 2) % 3] = qfrag(pair_nt(j + 2), pair_ks(j + 2));
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
           nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qr[j % 3],
@@ -427,14 +470,29 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       }
     }
   };
-  auto phase2 = [&](const SBuf& nx, const VSet& vf) -> bool {
+  // O^T += V^T . P^T for MFMA pair j of phase 2 (jj = 2 j, 2 j + 1).
+  auto pv_pair = [&](const VSet& vf, int j) {
+    const int dt0 = (2 * j) / NT, nt0 = (2 * j) % NT, dt1 = (2 * j + 1) / NT, nt1 = (2 * j + 1) % NT;
+    if constexpr (OA) {
+      mfma16x16x32_agpr2(o[dt0][nt0], vf[dt0], pb[nt0], o[dt1][nt1], vf[dt1], pb[nt1]);
+    } else {
+      o[dt0][nt0] = mfma16x16x32(vf[dt0], pb[nt0], o[dt0][nt0]);
+      o[dt1][nt1] = mfma16x16x32(vf[dt1], pb[nt1], o[dt1][nt1]);
+    }
+  };
+  // vn (OA): slabs of the V^T set to load next, each fragment requested
+  // into its registers right after the MFMAs that read it (which gives the
+  // load the rest of this phase and the next phase 1; requesting the K
+  // fragments of phase 1 the same way costs registers the loop does not
+  // have at head_dim 256 and spills, 10 % slower at c5).
+  auto phase2 = [&](const SBuf& nx, VSet& vf, gchar* vn) -> bool {
     grow = false;
 #pragma unroll
     for (int j = 0; j < P2; ++j) {
-#pragma unroll
-      for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
-        const int dt = jj / NT, nt = jj % NT;
-        o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+      pv_pair(vf, j);
+      if constexpr (OA) {
+        const int dt = (2 * j + 1) / NT;
+        if ((2 * j + 2) % NT == 0) vf[dt] = slab(vn, dt);
       }
 #pragma unroll
       for (int r = (j * RU + P2 - 1) / P2; r < ((j + 1) * RU + P2 - 1) / P2; ++r) rowmax_unit(nx, r);
@@ -455,9 +513,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   };
   auto pv = [&](const VSet& vf) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+    for (int j = 0; j < P2; ++j) pv_pair(vf, j);
   };
   // Phase 2 without SB: the P.V MFMAs row set by row set; once
   // row set nt' of P(u) has been read, row set nt' of P(u+1) is computed
@@ -508,6 +564,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     // 2000 cycles at head_dim 256).
     auto step1 = [&](SBuf& cur, SBuf& nxt, int u) {
       const int rk = blk_raw(u + 2), rm1 = blk_raw(u + 1);
+      asm volatile("" : "+v"(lane_b));
       phase1(cur, nxt, ka);
       load_k(uni(rk), clamp_u(u + 2) & 1, ka);
 #pragma unroll
@@ -517,8 +574,8 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
         pb[nt] = __builtin_bit_cast(bf16x8, pin);
       }
       mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
-      const bool moved = phase2(nxt, va);
-      load_v(uni(rm1), (u + 1) & 1, va);
+      const bool moved = phase2(nxt, va, v_ptr(uni(rm1), (u + 1) & 1));
+      if constexpr (!OA) load_v(uni(rm1), (u + 1) & 1, va);
       if (moved) rescale();
     };
     if (nv > 0) {
@@ -593,6 +650,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   }
 
   // ---- normalise and store ------------------------------------------------
+  drain_o();
   uint16_t* ob = out + b * so_b + h * so_h;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -645,7 +703,7 @@ constexpr int gen_waves() { return D > 128 ? 1 : 3; }
 // tile_order (optional): the (b, t) tiles heaviest first (attn_tile_order);
 // it enables the generations above.  Without it, one launch with tiles by t
 // descending.
-template <int D, int NT, bool QLDS, bool SB>
+template <int D, int NT, bool QLDS, bool SB, bool OA = false>
 static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                    const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                                    const uint16_t* vt, const int32_t* kv_idx,
@@ -661,7 +719,7 @@ static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h
   const size_t lds = static_cast<size_t>(WPT) *
                      pipe_wave_lds(D, NT, QLDS, k_slots, NB, rowmask != nullptr);
   if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
-  auto kern = attn_fwd_pipe_kernel<D, NT, QLDS, SB>;
+  auto kern = attn_fwd_pipe_kernel<D, NT, QLDS, SB, OA>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -37,6 +37,52 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Two MFMAs accumulating in AGPRs, c0 += a0 . b0 and c1 += a1 . b1 (the
+// accumulators never leave the AGPR file).  Written as inline assembly
+// because the compiler, built with MFMA results in VGPRs, would otherwise
+// place every accumulator there; its hazard recognizer does not look inside
+// the asm, so the wait states are explicit: s_nop 1 gives the two a VALU
+// write of an operand needs before an MFMA reads it (A, B, or the
+// accumulator after v_accvgpr_write), and agpr_drain() the ones a VALU read
+// of the results needs after the last MFMA.
+__device__ __forceinline__ void mfma16x16x32_agpr2(f32x4& c0, bf16x8 a0, bf16x8 b0, f32x4& c1,
+                                                   bf16x8 a1, bf16x8 b1) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\t"
+      "v_mfma_f32_16x16x32_bf16 %1, %4, %5, %1"
+      : "+a"(c0), "+a"(c1)
+      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
+}
+// Wait states between the last MFMA writing AGPR accumulators and any
+// other access to them (the compiler waits 8 after a 16x16x32 bf16 MFMA;
+// 24 here).  Callers pin the accumulators after it ("+a" on an empty asm)
+// so that no read of them is scheduled above it.
+__device__ __forceinline__ void agpr_drain() {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+}
+
+// Global-memory pointers with a wave-uniform (SGPR) base: 16-byte slab s of
+// a run of 1 KiB slabs at base is read at base + 4 KiB * (s / 4) (a scalar
+// add) + lane_b + 1 KiB * (s % 4) (the instruction's offset field, which
+// holds less than 4 KiB), so every load takes the SGPR-base form with one
+// 32-bit lane offset instead of a 64-bit address per lane in VGPRs.
+typedef const __attribute__((address_space(1))) char gchar;
+typedef const __attribute__((address_space(1))) bf16x8 gbf16x8;
+__device__ __forceinline__ gchar* uniform_gptr(gchar* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return reinterpret_cast<gchar*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+// Callers in loops refresh lane_b once per iteration with an empty volatile
+// asm: a 64-bit copy of it hoisted out of the loop would hide the 32-bit
+// offset that the SGPR-base form needs.
+__device__ __forceinline__ bf16x8 load_slab(gchar* base, uint32_t lane_b, int s) {
+  gchar* b4 = uniform_gptr(base + (s / 4) * 4096);
+  return *reinterpret_cast<gbf16x8*>(b4 + (lane_b + static_cast<uint32_t>(s % 4) * 1024u));
+}
+
 __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
