@@ -349,11 +349,11 @@ def measured_traffic(cfg_name):
 
 
 def attention_kernel_label(D, NB):
-    """The attn_fwd_pipe_kernel<D, NT, QLDS, SB> instance launch_attn_fwd
+    """The attn_fwd_pipe_kernel<D, NT, QLDS, SB, OA> instance launch_attn_fwd
     runs for 64-row tiles (csrc/attn_fwd.hip)."""
     if D == 256:
-        return "attn_fwd_pipe_kernel<256, 2, true, true>"
-    return f"attn_fwd_pipe_kernel<{D}, 4, false, false>"
+        return "attn_fwd_pipe_kernel<256, 4, true, true, true>"
+    return f"attn_fwd_pipe_kernel<{D}, 4, false, false, false>"
 
 
 def roofline(cfg_name, D, NB, tflops):
