@@ -10,8 +10,12 @@
  * Conventions
  *  - Pointers are device pointers (e.g. torch.Tensor.data_ptr()); the library
  *    never allocates or frees device memory and keeps no pointer after return.
- *  - Strides are in elements (int64).  bf16 operands need head_dim stride 1,
- *    16-byte aligned base pointers and other strides that are multiples of 8.
+ *  - Strides are in elements (int64).  The 16-bit tensors of a call (q, k, v,
+ *    the summary planes, out) share one element format, `dtype`:
+ *    UGBSA_DTYPE_BF16 or UGBSA_DTYPE_F16 — the reference runs in the model's
+ *    dtype (src/triton_block_attn.py:267-298, src/sparse_attention.py:588-748).
+ *    They need head_dim stride 1, 16-byte aligned base pointers and other
+ *    strides that are multiples of 8.
  *  - Every launch is asynchronous on `stream` (a hipStream_t; NULL = default
  *    stream).  No entry point synchronises the host.
  *  - Return value: 0 on success, > 0 a hipError_t from the launch, < 0 an
@@ -36,6 +40,7 @@ extern "C" {
 #define UGBSA_EDTYPE (-3)   /* unsupported element type */
 
 #define UGBSA_DTYPE_BF16 0
+#define UGBSA_DTYPE_F16 1
 
 #define UGBSA_MODE_MEAN 0   /* K-mean backbone (Selector.router_score "mean", mode "topk") */
 #define UGBSA_MODE_QUEST 1  /* Quest K-max/K-min backbone (mode "quest", router_score "quest") */
@@ -51,15 +56,15 @@ extern "C" {
 int ugbsa_abi_version(void);
 const char* ugbsa_last_error(void);
 
-/* Number of bf16 elements of the block-summary buffer [B, Hk, NB, P, D]
+/* Number of 16-bit elements of the block-summary buffer [B, Hk, NB, P, D]
  * (P = 2 for Quest, 3 for mean). */
 int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode);
 
-/* Kernel 1 — per-64-token-block K summaries of k [B, Hk, N, D] bf16.
+/* Kernel 1 — per-64-token-block K summaries of k [B, Hk, N, D] (dtype).
  * Replaces the summary step of _block_select_kv_idx_v2:
  * src/sparse_attention.py:618-622 (zero pad), :636-637 (amin/amax, Quest),
- * :646 (mean).  Output planes: Quest (K-max, K-min), mean (hi, mid, lo bf16
- * terms of the fp32 mean). */
+ * :646 (mean).  Output planes, in dtype: Quest (K-max, K-min), mean (hi, mid,
+ * lo terms of the fp32 mean). */
 int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                         int B, int Hk, int N, int D, int dtype, int mode, void* planes,
                         void* stream);
@@ -69,7 +74,8 @@ int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
  * Replaces src/sparse_attention.py:623-707 of _block_select_kv_idx_v2
  * (per-row scores :638-648, tile max :655-656, causal tile mask :660-666,
  * FMAX forcing :675-681, topk :697, margin :703-707).
- * q [B, H, M, D] bf16 (query head h uses KV head h / (H / Hk));
+ * q [B, H, M, D] in dtype, the planes' format (query head h uses KV head
+ * h / (H / Hk));
  * kv_idx out [B, H, Qt, k_slots] int32 contiguous, slots ordered by
  * (score desc, block asc); sigma out [B, H, Qt] fp32; tile_score (optional
  * diagnostic) out [B, H, Qt, NB] fp32 = the exact scores ranked.
@@ -190,7 +196,7 @@ int ugbsa_attn_fwd_rows(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                         void* out, int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d,
                         void* workspace, void* stream);
 
-/* Number of bf16 elements of the attention workspace: the K and V operand
+/* Number of 16-bit elements of the attention workspace: the K and V operand
  * copies of ugbsa_attn_prepare_kv (2 * B * Hk * NB * 64 * D). */
 int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D);
 
@@ -206,10 +212,11 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
 
 /* Kernel 3 — block-sparse causal attention over kv_idx.
  * Replaces block_sparse_attn_v2 (src/triton_block_attn.py:267-298) and its
- * kernel _fwd_kernel_v2 (:184-264).  q [B, H, M, D], k/v [B, Hk, N, D] bf16
+ * kernel _fwd_kernel_v2 (:184-264).  q [B, H, M, D], k/v [B, Hk, N, D] in dtype
  * (Hk may equal H, as after repeat_kv), kv_idx [B, H, Qt, k_slots] int32 with
  * Qt = ceil(M / block_m), block_m 64 or 32, sentinel NB skipped; out
- * [B, H, M, D] bf16 with arbitrary strides (head_dim stride 1).  v may be
+ * [B, H, M, D] in dtype (P rounded to dtype before P.V, as the reference's
+ * p.to(v.dtype)) with arbitrary strides (head_dim stride 1).  v may be
  * NULL when workspace already holds ugbsa_attn_prepare_kv(k, v, block_m);
  * otherwise the preparation runs first, on the same stream.  scale must be
  * finite and nonzero (UGBSA_EARG otherwise). */

@@ -49,11 +49,11 @@ def tiny_qwen35_moe():
 FAMILIES = {"qwen2": (tiny_qwen2, 2), "qwen3_5_moe": (tiny_qwen35_moe, 1)}
 
 
-def build(make_cfg, impl, seed=0):
+def build(make_cfg, impl, seed=0, dtype=torch.bfloat16):
     from transformers import AutoModelForCausalLM
     torch.manual_seed(seed)
     model = AutoModelForCausalLM.from_config(make_cfg(), attn_implementation=impl)
-    return model.to(device=DEV, dtype=torch.bfloat16).eval()
+    return model.to(device=DEV, dtype=dtype).eval()
 
 
 def input_ids(seed=1):
@@ -101,10 +101,21 @@ def sel_state():
 @pytest.mark.parametrize("family", sorted(FAMILIES))
 @pytest.mark.parametrize("policy", ["router_quest", "topk"])
 def test_model_prefill_layers_match_oracle(hip_lib, sel_state, family, policy):
-    print(f"[case] hf {family} {policy}", flush=True)
+    check_prefill_layers(family, policy, torch.bfloat16)
+
+
+@pytest.mark.parametrize("policy", ["router_quest", "topk"])
+def test_qwen2_fp16_prefill_layers_match_oracle(hip_lib, sel_state, policy):
+    """The same drop-in check on a model loaded in fp16: q / k / v reach the
+    selector and kernel 3 as fp16 and the output comes back in fp16."""
+    check_prefill_layers("qwen2", policy, torch.float16)
+
+
+def check_prefill_layers(family, policy, dtype):
+    print(f"[case] hf {family} {policy} {dtype}", flush=True)
     make_cfg, n_full = FAMILIES[family]
     sel_policy(policy)
-    model = build(make_cfg, "block_sparse")
+    model = build(make_cfg, "block_sparse", dtype=dtype)
     # capture attention outputs too: hook the dispatcher's kernel call
     outs = []
     orig_attn = sa.block_sparse_attn_v2
@@ -126,6 +137,7 @@ def test_model_prefill_layers_match_oracle(hip_lib, sel_state, family, policy):
     cfg = OS.SelectorConfig.from_selector(sa.SEL)
     for li, ((q, k, scaling, kv), (q2, k2, v2, kv2, o, scale)) in enumerate(zip(cap.calls, outs)):
         assert torch.equal(kv, kv2)
+        assert q.dtype == k.dtype == v2.dtype == o.dtype == dtype
         assert q.shape[1] == 4 and k.shape[1] == 2          # GQA reaches the kernels un-repeated
         res = sa.select_v2(q, k, scaling, want_tile_score=True)
         sel = OS.select_from_tile_scores(res.tile_score.cpu().numpy(), cfg)

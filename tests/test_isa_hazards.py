@@ -29,7 +29,9 @@ sys.path.insert(0, ROOT)
 
 import __graft_entry__ as G  # noqa: E402
 
-KERNEL = "_ZN5ugbsa20attn_fwd_pipe_kernelILi256ELi4ELb1ELb1ELb1E"
+# the head_dim-256 instances, bf16 and fp16
+KERNELS = ["_ZN5ugbsa20attn_fwd_pipe_kernelINS_8ElemBf16ELi256ELi4ELb1ELb1ELb1E",
+           "_ZN5ugbsa20attn_fwd_pipe_kernelINS_7ElemF16ELi256ELi4ELb1ELb1ELb1E"]
 MIN_WAIT_STATES = 18
 
 
@@ -45,9 +47,9 @@ def asm(tmp_path_factory):
     return (d / "k.s").read_text()
 
 
-def kernel_body(text):
+def kernel_body(text, kernel):
     lines = text.split("\n")
-    start = next(i for i, l in enumerate(lines) if l.startswith(KERNEL) and l.split(";")[0].rstrip().endswith(":"))
+    start = next(i for i, l in enumerate(lines) if l.startswith(kernel) and l.split(";")[0].rstrip().endswith(":"))
     end = next(i for i in range(start, len(lines)) if lines[i].startswith(".Lfunc_end"))
     return lines[start + 1:end]
 
@@ -139,8 +141,9 @@ def agpr_hazards(body):
     return bad, mfmas, checked
 
 
-def test_agpr_accesses_wait_for_the_matrix_cores(asm):
-    bad, mfmas, checked = agpr_hazards(kernel_body(asm))
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_agpr_accesses_wait_for_the_matrix_cores(asm, kernel):
+    bad, mfmas, checked = agpr_hazards(kernel_body(asm, kernel))
     assert not bad, bad[:5]
     assert mfmas >= 64 and checked >= 256, (mfmas, checked)
 
@@ -160,8 +163,9 @@ def test_hazard_check_flags_an_early_read():
     assert agpr_hazards(loop[:-2] + drained[4:9] + loop[-2:])[0] == []
 
 
-def test_asm_mfma_pairs_start_with_two_wait_states(asm):
-    body = "\n".join(kernel_body(asm))
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_asm_mfma_pairs_start_with_two_wait_states(asm, kernel):
+    body = "\n".join(kernel_body(asm, kernel))
     blocks = re.findall(r";;#ASMSTART\n(.*?);;#ASMEND", body, re.S)
     pairs = [b for b in blocks if "v_mfma" in b]
     assert pairs
@@ -170,12 +174,13 @@ def test_asm_mfma_pairs_start_with_two_wait_states(asm):
         assert ins[0] == "s_nop 1", ins
 
 
-def test_no_scratch_and_no_packed_fp32(asm):
-    body = "\n".join(kernel_body(asm))
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_no_scratch_and_no_packed_fp32(asm, kernel):
+    body = "\n".join(kernel_body(asm, kernel))
     assert not re.search(r"\bv_pk_(add|mul|fma)_f32\b", body)
     assert "scratch_" not in body
     meta = asm[asm.index(".amdgpu_metadata"):]
-    entries = [e for e in re.split(r"\n  - \.", meta) if re.search(r"\.name:\s+" + KERNEL, e)]
+    entries = [e for e in re.split(r"\n  - \.", meta) if re.search(r"\.name:\s+" + kernel, e)]
     assert len(entries) == 1
     m = re.search(r"\.private_segment_fixed_size:\s+(\d+)", entries[0])
     assert m and int(m.group(1)) == 0

@@ -21,7 +21,7 @@ import torch
 LIB_NAME = "libugbsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-DTYPE_BF16 = 0
+DTYPE_BF16, DTYPE_F16 = 0, 1
 MODE_MEAN, MODE_QUEST = 0, 1
 GRAIN_CELL, GRAIN_ROW = 0, 1
 ROUTER_ABS, ROUTER_QUANTILE = 0, 1
@@ -93,6 +93,13 @@ def check(rc: int, what: str) -> None:
     if rc < 0:
         raise AssertionError(f"{what}: {msg}")
     raise RuntimeError(f"{what}: HIP error {rc}: {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    """The C ABI's element-format code of a 16-bit torch dtype; the kernels
+    run in the caller's dtype as the reference does, bf16 or fp16."""
+    assert dtype in (torch.bfloat16, torch.float16), f"bf16 or fp16 required, got {dtype}"
+    return DTYPE_F16 if dtype == torch.float16 else DTYPE_BF16
 
 
 def stream_ptr(device: torch.device) -> int:

@@ -32,25 +32,30 @@ import torch.nn.functional as F
 import _capi
 
 
-def _bf16_operand(name, t):
+def _operand(name, t, dtype=None):
+    """A 16-bit device operand the kernels can read (head_dim stride 1,
+    16-byte aligned rows); dtype: the format the call's other tensors have."""
     assert t.is_cuda, f"{name} must be a HIP device tensor"
-    assert t.dtype == torch.bfloat16, f"{name}: bf16 required, got {t.dtype}"
+    _capi.dtype_code(t.dtype)
+    assert dtype is None or t.dtype == dtype, f"{name}: {dtype} required (as q), got {t.dtype}"
     if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
         t = t.contiguous()
     return t
 
 
-def attn_workspace(B: int, Hk: int, N: int, D: int, device) -> torch.Tensor:
-    """Workspace of ``ugbsa_attn_fwd`` (V transposed per 64-key block)."""
+def attn_workspace(B: int, Hk: int, N: int, D: int, device, dtype=torch.bfloat16) -> torch.Tensor:
+    """Workspace of ``ugbsa_attn_fwd`` (K and V in the kernel's operand
+    order, 16-bit elements, then the tile schedule)."""
     n = _capi.lib().ugbsa_attn_workspace_elems(B, Hk, N, D)
-    return torch.empty(n, dtype=torch.bfloat16, device=device)
+    return torch.empty(n, dtype=dtype, device=device)
 
 
 def block_sparse_attn_v2(q, k, v, kv_idx, scale, block_n=64, block_m=64,
                          num_warps=4, num_stages=1, out=None, workspace=None):
-    """Per-tile-selection block-sparse causal attention (HIP, bf16 MFMA).
+    """Per-tile-selection block-sparse causal attention (HIP, bf16 / fp16 MFMA).
 
-    q : [B, H, M, D] bf16; k, v : [B, Hk, N, D] bf16 (Hk == H or H % Hk == 0)
+    q : [B, H, M, D] bf16 or fp16; k, v : [B, Hk, N, D] in q's dtype (Hk == H
+    or H % Hk == 0)
     kv_idx : [B, H, ceil(M / block_m), MAX_KEPT] int32, sentinel = NB skipped
     Returns out [B, H, M, D] (``out`` if given).
     """
@@ -63,23 +68,23 @@ def block_sparse_attn_v2(q, k, v, kv_idx, scale, block_n=64, block_m=64,
     Hk, N = k.shape[1], k.shape[2]
     assert H % Hk == 0, "query heads must be a multiple of KV heads"
     assert kv_idx.dim() == 4 and tuple(kv_idx.shape[:3]) == (B, H, (M + block_m - 1) // block_m)
-    q = _bf16_operand("q", q)
-    k = _bf16_operand("k", k)
-    v = _bf16_operand("v", v)
+    q = _operand("q", q)
+    k = _operand("k", k, q.dtype)
+    v = _operand("v", v, q.dtype)
     if kv_idx.stride(-1) != 1:
         kv_idx = kv_idx.contiguous()
     if out is None:
         out = torch.empty_like(q)
     assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
     if workspace is None:
-        workspace = attn_workspace(B, Hk, N, D, q.device)
+        workspace = attn_workspace(B, Hk, N, D, q.device, q.dtype)
     lib = _capi.lib()
     rc = lib.ugbsa_attn_fwd(
         q.data_ptr(), *q.stride(),
         k.data_ptr(), *k.stride(),
         v.data_ptr(), *v.stride(),
         kv_idx.data_ptr(), *kv_idx.stride(),
-        B, H, Hk, M, N, D, _capi.DTYPE_BF16, kv_idx.shape[2], kv_idx.shape[3], block_m,
+        B, H, Hk, M, N, D, _capi.dtype_code(q.dtype), kv_idx.shape[2], kv_idx.shape[3], block_m,
         float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(),
         _capi.stream_ptr(q.device))
     _capi.check(rc, "block_sparse_attn_v2")
@@ -110,9 +115,9 @@ def keep_kv_idx(keep, block_m=64, want_rowmask=True):
 
 def block_sparse_attn(q, k, v, keep, scale, block_n=64, block_m=64,
                       num_warps=4, num_stages=1, out=None, workspace=None):
-    """Per-row-selection block-sparse causal attention (HIP, bf16 MFMA).
+    """Per-row-selection block-sparse causal attention (HIP, bf16 / fp16 MFMA).
 
-    q : [B, H, M, D] bf16; k, v : [B, Hk, N, D] bf16; keep : [B, H, M, NB]
+    q : [B, H, M, D] bf16 or fp16; k, v : [B, Hk, N, D] in q's dtype; keep : [B, H, M, NB]
     bool (True = the row attends to the block).  Same contract as
     src/triton_block_attn.py:149-182: per Q tile the union of its rows'
     blocks is visited in ascending order (``_compute_kv_idx``) and each row
@@ -128,20 +133,20 @@ def block_sparse_attn(q, k, v, keep, scale, block_n=64, block_m=64,
     assert H % Hk == 0, "query heads must be a multiple of KV heads"
     assert tuple(keep.shape[:3]) == (B, H, M), "keep [B, H, M, NB] expected"
     kv, rm, max_kept = keep_kv_idx(keep, block_m)
-    q = _bf16_operand("q", q)
-    k = _bf16_operand("k", k)
-    v = _bf16_operand("v", v)
+    q = _operand("q", q)
+    k = _operand("k", k, q.dtype)
+    v = _operand("v", v, q.dtype)
     if out is None:
         out = torch.empty_like(q)
     assert out.shape == q.shape and out.dtype == q.dtype and out.stride(-1) == 1
     if workspace is None:
-        workspace = attn_workspace(B, Hk, N, D, q.device)
+        workspace = attn_workspace(B, Hk, N, D, q.device, q.dtype)
     rc = _capi.lib().ugbsa_attn_fwd_rows(
         q.data_ptr(), *q.stride(),
         k.data_ptr(), *k.stride(),
         v.data_ptr(), *v.stride(),
         kv.data_ptr(), rm.data_ptr(), *kv.stride(),
-        B, H, Hk, M, N, D, _capi.DTYPE_BF16, kv.shape[2], max_kept, block_m,
+        B, H, Hk, M, N, D, _capi.dtype_code(q.dtype), kv.shape[2], max_kept, block_m,
         float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(),
         _capi.stream_ptr(q.device))
     _capi.check(rc, "block_sparse_attn")

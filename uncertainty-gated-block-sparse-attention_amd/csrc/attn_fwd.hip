@@ -275,7 +275,7 @@ __device__ __forceinline__ int key_of(int mt, int R) {
 // 16 * NT * WPT = 32 rows, each wave 16 * NT of them, and every wave visits
 // every listed block.  V^T of the current block is requested before its S^T
 // product and K of the next visited block right after it.
-template <int D, int NT, int WPT>
+template <typename E, int D, int NT, int WPT>
 __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) st[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], st[mt][nt]);
+        for (int nt = 0; nt < NT; ++nt) st[mt][nt] = E::mfma(kf[mt][ks], qf[nt][ks], st[mt][nt]);
 
     const int s_next = next_slot(s + 1);
     if (s_next < k_slots) load_k(block_at(s_next), kf);
@@ -458,17 +458,17 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         u32x4 w;
-        w[0] = cvt_pk_bf16(st[2 * s2][nt][0], st[2 * s2][nt][1]);
-        w[1] = cvt_pk_bf16(st[2 * s2][nt][2], st[2 * s2][nt][3]);
-        w[2] = cvt_pk_bf16(st[2 * s2 + 1][nt][0], st[2 * s2 + 1][nt][1]);
-        w[3] = cvt_pk_bf16(st[2 * s2 + 1][nt][2], st[2 * s2 + 1][nt][3]);
+        w[0] = E::pack2(st[2 * s2][nt][0], st[2 * s2][nt][1]);
+        w[1] = E::pack2(st[2 * s2][nt][2], st[2 * s2][nt][3]);
+        w[2] = E::pack2(st[2 * s2 + 1][nt][0], st[2 * s2 + 1][nt][1]);
+        w[3] = E::pack2(st[2 * s2 + 1][nt][2], st[2 * s2 + 1][nt][3]);
         pb[nt] = __builtin_bit_cast(bf16x8, w);
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const bf16x8 vv = vf[dt][s2];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) o[dt][nt] = mfma16x16x32(vv, pb[nt], o[dt][nt]);
+        for (int nt = 0; nt < NT; ++nt) o[dt][nt] = E::mfma(vv, pb[nt], o[dt][nt]);
       }
     }
     s = s_next;
@@ -486,15 +486,15 @@ __global__ __launch_bounds__(64 * WPT) void attn_fwd_kernel(
     if (row < M) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint32_t w0 = cvt_pk_bf16(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
-        const uint32_t w1 = cvt_pk_bf16(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
+        const uint32_t w0 = E::pack2(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
+        const uint32_t w1 = E::pack2(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
         *reinterpret_cast<uint2*>(ob + row * so_m + 16 * dt + 4 * g4) = make_uint2(w0, w1);
       }
     }
   }
 }
 
-template <int D, int NT, int WPT>
+template <typename E, int D, int NT, int WPT>
 static hipError_t launch_attn_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                 const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                                 const uint16_t* vt, const int32_t* kv_idx,
@@ -506,19 +506,21 @@ static hipError_t launch_attn_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, i
   const int grp = H / Hk;
   const int units = B * Hk * Qt;
   const int64_t wgs = 8LL * grp * ((units + 7) / 8);
-  attn_fwd_kernel<D, NT, WPT><<<dim3(static_cast<unsigned>(wgs)), 64 * WPT, 0, stream>>>(
+  attn_fwd_kernel<E, D, NT, WPT><<<dim3(static_cast<unsigned>(wgs)), 64 * WPT, 0, stream>>>(
       q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, Hk, M,
       N, NB, Qt, k_slots, scale * kLog2e, out, so_b, so_h, so_m, units, grp);
   return hipGetLastError();
 }
 
-hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
-                           const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                           const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
-                           int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
-                           int D, int Qt, int k_slots, int block_m, float scale, uint16_t* out,
-                           int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream,
-                           const uint64_t* rowmask, int32_t* order_ws) {
+template <typename E>
+static hipError_t launch_attn_fwd_e(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                                    const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                                    const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
+                                    int64_t si_h, int64_t si_t, int B, int H, int Hk, int M,
+                                    int N, int D, int Qt, int k_slots, int block_m, float scale,
+                                    uint16_t* out, int64_t so_b, int64_t so_h, int64_t so_m,
+                                    hipStream_t stream, const uint64_t* rowmask,
+                                    int32_t* order_ws) {
   if (uses_pipe(D, block_m)) {   // the pipelined kernel (its K/V operand layout is prepared)
     if (k_slots > kPipeMaxSlots) return hipErrorInvalidValue;
     const int NBk = (N + kBlock - 1) / kBlock;
@@ -530,14 +532,14 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
       tile_order = order_ws + static_cast<int64_t>(B) * Qt;
     }
     if (D == 256)
-      return launch_attn_pipe256(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b,
+      return launch_attn_pipe256(E::code, q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b,
                                  si_h, si_t, B, H, Hk, M, N, Qt, k_slots, scale, out, so_b, so_h,
                                  so_m, stream, tile_order);
     if (D == 128)
-      return launch_attn_pipe<128, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
+      return launch_attn_pipe<E, 128, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                           rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
                                           scale, out, so_b, so_h, so_m, stream, tile_order);
-    return launch_attn_pipe<64, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
+    return launch_attn_pipe<E, 64, 4, false, false>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
                                        rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt, k_slots,
                                        scale, out, so_b, so_h, so_m, stream, tile_order);
   }
@@ -547,12 +549,28 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
   q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, H, Hk, M, \
       N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream
   switch (D) {
-    case 64: return launch_attn_t<64, 2, 1>(UGBSA_ATTN32_ARGS);
-    case 128: return launch_attn_t<128, 2, 1>(UGBSA_ATTN32_ARGS);
-    case 256: return launch_attn_t<256, 1, 2>(UGBSA_ATTN32_ARGS);
+    case 64: return launch_attn_t<E, 64, 2, 1>(UGBSA_ATTN32_ARGS);
+    case 128: return launch_attn_t<E, 128, 2, 1>(UGBSA_ATTN32_ARGS);
+    case 256: return launch_attn_t<E, 256, 1, 2>(UGBSA_ATTN32_ARGS);
   }
 #undef UGBSA_ATTN32_ARGS
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                           const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                           const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
+                           int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
+                           int D, int elem, int Qt, int k_slots, int block_m, float scale,
+                           uint16_t* out, int64_t so_b, int64_t so_h, int64_t so_m,
+                           hipStream_t stream, const uint64_t* rowmask, int32_t* order_ws) {
+  if (elem == ElemF16::code)
+    return launch_attn_fwd_e<ElemF16>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b,
+                                      si_h, si_t, B, H, Hk, M, N, D, Qt, k_slots, block_m, scale,
+                                      out, so_b, so_h, so_m, stream, rowmask, order_ws);
+  return launch_attn_fwd_e<ElemBf16>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, si_b,
+                                     si_h, si_t, B, H, Hk, M, N, D, Qt, k_slots, block_m, scale,
+                                     out, so_b, so_h, so_m, stream, rowmask, order_ws);
 }
 
 }  // namespace ugbsa

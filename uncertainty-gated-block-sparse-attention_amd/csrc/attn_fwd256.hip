@@ -7,17 +7,21 @@
 
 namespace ugbsa {
 
-hipError_t launch_attn_pipe256(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
-                               const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                               const uint16_t* vt, const int32_t* kv_idx,
+hipError_t launch_attn_pipe256(int elem, const uint16_t* q, int64_t sq_b, int64_t sq_h,
+                               int64_t sq_m, const uint16_t* k, int64_t sk_b, int64_t sk_h,
+                               int64_t sk_n, const uint16_t* vt, const int32_t* kv_idx,
                                const uint64_t* rowmask, int64_t si_b, int64_t si_h,
                                int64_t si_t, int B, int H, int Hk, int M, int N, int Qt,
                                int k_slots, float scale, uint16_t* out, int64_t so_b,
                                int64_t so_h, int64_t so_m, hipStream_t stream,
                                const int32_t* tile_order) {
-  return launch_attn_pipe<256, 4, true, true, true>(q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx,
-                                           rowmask, si_b, si_h, si_t, B, H, Hk, M, N, Qt,
-                                           k_slots, scale, out, so_b, so_h, so_m, stream, tile_order);
+  if (elem == ElemF16::code)
+    return launch_attn_pipe<ElemF16, 256, 4, true, true, true>(
+        q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, H, Hk,
+        M, N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream, tile_order);
+  return launch_attn_pipe<ElemBf16, 256, 4, true, true, true>(
+      q, sq_b, sq_h, sq_m, k, sk_b, sk_h, sk_n, vt, kv_idx, rowmask, si_b, si_h, si_t, B, H, Hk, M,
+      N, Qt, k_slots, scale, out, so_b, so_h, so_m, stream, tile_order);
 }
 
 }  // namespace ugbsa

@@ -43,7 +43,7 @@ __host__ __device__ inline int pipe_wave_lds(int D, int NT, bool qlds, int k_slo
   return (bytes + 15) / 16 * 16;
 }
 
-template <int D, int NT, bool QLDS, bool SB, bool OA>
+template <typename E, int D, int NT, bool QLDS, bool SB, bool OA>
 __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     const int nt = e / 8, kk = e % 8, mt = kk / 4, i = kk % 4;
     p[nt][kk] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][nt][i], sl2, -m[nt]));
     sum[nt] = kk == 0 ? p[nt][0] : sum[nt] + p[nt][kk];
-    if (kk & 1) w[nt][kk / 2] = cvt_pk_bf16(p[nt][kk - 1], p[nt][kk]);
+    if (kk & 1) w[nt][kk / 2] = E::pack2(p[nt][kk - 1], p[nt][kk]);
     if (kk == 7) {
       if constexpr (SB) l[nt] += sum[nt];
       pb[nt] = __builtin_bit_cast(bf16x8, u32x4{w[nt][0], w[nt][1], w[nt][2], w[nt][3]});
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          st[mt][nt] = mfma16x16x32(kf[mt][ks], qfrag(nt, ks), ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[mt][nt]);
+          st[mt][nt] = E::mfma(kf[mt][ks], qfrag(nt, ks), ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[mt][nt]);
   };
 
   // The two phases of a step are woven by hand (one wave per SIMD issues in
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
         if constexpr (j + 2 < P1) qr[(j + 2) % 3] = qfrag(pair_nt(j + 2), pair_ks(j + 2));
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
-          nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qr[j % 3],
+          nxt[mt][nt] = E::mfma(kf[mt][ks], qr[j % 3],
                                      ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
 #pragma unroll
         for (int e = E1ST + (j * NE1 + P1 - 1) / P1; e < E1ST + ((j + 1) * NE1 + P1 - 1) / P1; ++e)
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
 #pragma unroll
         for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
           const int ks = jj / (2 * NT), mt = (jj / NT) & 1, nt = jj % NT;
-          nxt[mt][nt] = mfma16x16x32(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
+          nxt[mt][nt] = E::mfma(kf[mt][ks], qf[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : nxt[mt][nt]);
         }
 #pragma unroll
         for (int e = E1ST + (j * NE1 + P1 - 1) / P1; e < E1ST + ((j + 1) * NE1 + P1 - 1) / P1; ++e)
@@ -474,10 +474,10 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   auto pv_pair = [&](const VSet& vf, int j) {
     const int dt0 = (2 * j) / NT, nt0 = (2 * j) % NT, dt1 = (2 * j + 1) / NT, nt1 = (2 * j + 1) % NT;
     if constexpr (OA) {
-      mfma16x16x32_agpr2(o[dt0][nt0], vf[dt0], pb[nt0], o[dt1][nt1], vf[dt1], pb[nt1]);
+      mfma16x16x32_agpr2<E>(o[dt0][nt0], vf[dt0], pb[nt0], o[dt1][nt1], vf[dt1], pb[nt1]);
     } else {
-      o[dt0][nt0] = mfma16x16x32(vf[dt0], pb[nt0], o[dt0][nt0]);
-      o[dt1][nt1] = mfma16x16x32(vf[dt1], pb[nt1], o[dt1][nt1]);
+      o[dt0][nt0] = E::mfma(vf[dt0], pb[nt0], o[dt0][nt0]);
+      o[dt1][nt1] = E::mfma(vf[dt1], pb[nt1], o[dt1][nt1]);
     }
   };
   // vn (OA): slabs of the V^T set to load next, each fragment requested
@@ -526,7 +526,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
 #pragma unroll
       for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
         const int nt = jj / DT, dt = jj % DT;
-        o[dt][nt] = mfma16x16x32(vf[dt], pb[nt], o[dt][nt]);
+        o[dt][nt] = E::mfma(vf[dt], pb[nt], o[dt][nt]);
       }
       if (j >= PPN && j < PPN * (NT / 2 + 1)) {
 #pragma unroll
@@ -661,8 +661,8 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     if (row < M) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint32_t w0 = cvt_pk_bf16(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
-        const uint32_t w1 = cvt_pk_bf16(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
+        const uint32_t w0 = E::pack2(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
+        const uint32_t w1 = E::pack2(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
         *reinterpret_cast<uint2*>(ob + row * so_m + 16 * dt + 4 * g4) = make_uint2(w0, w1);
       }
     }
@@ -703,7 +703,7 @@ constexpr int gen_waves() { return D > 128 ? 1 : 3; }
 // tile_order (optional): the (b, t) tiles heaviest first (attn_tile_order);
 // it enables the generations above.  Without it, one launch with tiles by t
 // descending.
-template <int D, int NT, bool QLDS, bool SB, bool OA = false>
+template <typename E, int D, int NT, bool QLDS, bool SB, bool OA = false>
 static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                    const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                                    const uint16_t* vt, const int32_t* kv_idx,
@@ -719,7 +719,7 @@ static hipError_t launch_attn_pipe(const uint16_t* q, int64_t sq_b, int64_t sq_h
   const size_t lds = static_cast<size_t>(WPT) *
                      pipe_wave_lds(D, NT, QLDS, k_slots, NB, rowmask != nullptr);
   if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
-  auto kern = attn_fwd_pipe_kernel<D, NT, QLDS, SB, OA>;
+  auto kern = attn_fwd_pipe_kernel<E, D, NT, QLDS, SB, OA>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -46,7 +46,8 @@ int check_bf16_operand(const char* name, const void* p, int64_t s_b, int64_t s_h
 }
 
 int check_dims(int B, int H, int Hk, int D, int dtype) {
-  if (dtype != UGBSA_DTYPE_BF16) return fail(UGBSA_EDTYPE, "only bf16 tensors are supported (dtype code %d)", dtype);
+  if (dtype != UGBSA_DTYPE_BF16 && dtype != UGBSA_DTYPE_F16)
+    return fail(UGBSA_EDTYPE, "only bf16 and fp16 tensors are supported (dtype code %d)", dtype);
   if (B < 1 || H < 1 || Hk < 1) return fail(UGBSA_EARG, "B, H, Hk must be positive");
   if (H % Hk) return fail(UGBSA_EARG, "query heads (%d) must be a multiple of key heads (%d)", H, Hk);
   if (D != 64 && D != 128 && D != 256) return fail(UGBSA_EARG, "head_dim %d not supported (64, 128, 256)", D);
@@ -90,7 +91,7 @@ int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
   if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
   if (planes == nullptr) return fail(UGBSA_EARG, "planes is null");
   return hip_result(ugbsa::launch_block_summary(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, B, Hk, N, D,
-                                                mode, static_cast<uint16_t*>(planes),
+                                                dtype, mode, static_cast<uint16_t*>(planes),
                                                 static_cast<hipStream_t>(stream)),
                     "block_summary");
 }
@@ -117,7 +118,7 @@ int ugbsa_select(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_
   if (sigma != nullptr && k_base >= k_slots) return fail(UGBSA_EARG, "sigma needs k_base < k_slots");
   return hip_result(ugbsa::launch_select(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
                                          static_cast<const uint16_t*>(planes), B, H, Hk, M, N, D,
-                                         mode, scaling, k_base, k_slots, sigma != nullptr, kv_idx,
+                                         dtype, mode, scaling, k_base, k_slots, sigma != nullptr, kv_idx,
                                          sigma, tile_score, static_cast<hipStream_t>(stream)),
                     "select");
 }
@@ -154,10 +155,10 @@ int ugbsa_score_dump(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, in
   dump.dump = 1;
   const uint16_t* q16 = static_cast<const uint16_t*>(q);
   const uint16_t* p16 = static_cast<const uint16_t*>(planes);
-  hipError_t e = ugbsa::launch_select(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, mode, scaling,
+  hipError_t e = ugbsa::launch_select(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, dtype, mode, scaling,
                                       k_b, rho_k + 1, 0, nullptr, nullptr, tile_score, st, &dump);
   if (e != hipSuccess) return hip_result(e, "score_dump select");
-  return hip_result(ugbsa::launch_score_tau(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, mode,
+  return hip_result(ugbsa::launch_score_tau(q16, sq_b, sq_h, sq_m, p16, B, H, Hk, M, N, D, dtype, mode,
                                             scaling, tau_hat, st),
                     "score_dump tau");
 }
@@ -285,7 +286,7 @@ int select_mask_impl(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, in
     aux.rows_t1 = t1;
     hipError_t e = ugbsa::launch_select(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
                                         static_cast<const uint16_t*>(planes), B, H, Hk, M, N, D,
-                                        mode, scaling, 1, 1, 0, nullptr, nullptr, nullptr, st, &aux);
+                                        dtype, mode, scaling, 1, 1, 0, nullptr, nullptr, nullptr, st, &aux);
     if (e != hipSuccess) return hip_result(e, "select_mask row scores");
     ugbsa::RowsArgs a;
     a.scores = workspace;
@@ -348,7 +349,7 @@ int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int
   }
   return hip_result(ugbsa::launch_attn_fwd(static_cast<const uint16_t*>(q), sq_b, sq_h, sq_m,
                                            static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, vt,
-                                           kv_idx, si_b, si_h, si_t, B, H, Hk, M, N, D, Qt,
+                                           kv_idx, si_b, si_h, si_t, B, H, Hk, M, N, D, dtype, Qt,
                                            k_slots, block_m, scale, static_cast<uint16_t*>(out),
                                            so_b, so_h, so_m, st, rowmask,
                                            reinterpret_cast<int32_t*>(vt + kv_copy_elems(B, Hk, N, D))),

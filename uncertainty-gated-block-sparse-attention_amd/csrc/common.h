@@ -7,8 +7,11 @@
 //    (slots 8*g4 .. 8*g4+7); it receives C[4*g4 + i][r16], i = 0..3.  Any
 //    consistent relabelling of the contraction slots between A and B gives the
 //    same product, which the kernels use to permute keys freely;
-//  * bf16 tensors are read with 16-byte vector loads, so the innermost (D)
-//    stride must be 1 and row strides multiples of 8 elements.
+//  * 16-bit tensors (bf16 or fp16, one format per call: ElemBf16 / ElemF16
+//    below) are read with 16-byte vector loads, so the innermost (D) stride
+//    must be 1 and row strides multiples of 8 elements.  In registers and
+//    LDS eight such elements travel as a bf16x8 whatever their format; the
+//    format's MFMA and conversions interpret them.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -35,31 +38,6 @@ constexpr float kLazyLog2 = 8.0f;
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Two MFMAs accumulating in AGPRs, c0 += a0 . b0 and c1 += a1 . b1 (the
-// accumulators never leave the AGPR file).  Written as inline assembly
-// because the compiler, built with MFMA results in VGPRs, would otherwise
-// place every accumulator there; its hazard recognizer does not look inside
-// the asm, so the wait states are explicit: s_nop 1 gives the two a VALU
-// write of an operand needs before an MFMA reads it (A, B, or the
-// accumulator after v_accvgpr_write), and agpr_drain() the ones a VALU read
-// of the results needs after the last MFMA.
-__device__ __forceinline__ void mfma16x16x32_agpr2(f32x4& c0, bf16x8 a0, bf16x8 b0, f32x4& c1,
-                                                   bf16x8 a1, bf16x8 b1) {
-  asm volatile(
-      "s_nop 1\n\t"
-      "v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\t"
-      "v_mfma_f32_16x16x32_bf16 %1, %4, %5, %1"
-      : "+a"(c0), "+a"(c1)
-      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
-}
-// Wait states between the last MFMA writing AGPR accumulators and any
-// other access to them (the compiler waits 8 after a 16x16x32 bf16 MFMA;
-// 24 here).  Callers pin the accumulators after it ("+a" on an empty asm)
-// so that no read of them is scheduled above it.
-__device__ __forceinline__ void agpr_drain() {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
 }
 
 // Global-memory pointers with a wave-uniform (SGPR) base: 16-byte slab s of
@@ -122,6 +100,77 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
   return __builtin_bit_cast(uint32_t, h);
+}
+
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Element formats of the 16-bit tensors (Q, K, V, the summary planes and the
+// attention output of one call share one).  Products of two 16-bit values
+// are exact in fp32 for both, so the fp32-accumulated scores and S = Q.K^T
+// follow the same arithmetic in either format.
+struct ElemBf16 {
+  static constexpr int code = 0;
+  __device__ static __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // round-to-nearest-even pair (lo = a)
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  }
+  __device__ static __forceinline__ float to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+  __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_bf16(f); }
+};
+struct ElemF16 {
+  static constexpr int code = 1;
+  __device__ static __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  }
+  __device__ static __forceinline__ float to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xFFFFu)));
+  }
+  __device__ static __forceinline__ uint16_t from_f32(float f) {
+    return static_cast<uint16_t>(pack2(f, 0.f) & 0xFFFFu);
+  }
+};
+
+// Two MFMAs accumulating in AGPRs, c0 += a0 . b0 and c1 += a1 . b1 (the
+// accumulators never leave the AGPR file).  Written as inline assembly
+// because the compiler, built with MFMA results in VGPRs, would otherwise
+// place every accumulator there; its hazard recognizer does not look inside
+// the asm, so the wait states are explicit: s_nop 1 gives the two a VALU
+// write of an operand needs before an MFMA reads it (A, B, or the
+// accumulator after v_accvgpr_write), and agpr_drain() the ones a VALU read
+// of the results needs after the last MFMA.
+template <typename E>
+__device__ __forceinline__ void mfma16x16x32_agpr2(f32x4& c0, bf16x8 a0, bf16x8 b0, f32x4& c1,
+                                                   bf16x8 a1, bf16x8 b1) {
+  if constexpr (E::code == ElemF16::code) {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mfma_f32_16x16x32_f16 %0, %2, %3, %0\n\t"
+        "v_mfma_f32_16x16x32_f16 %1, %4, %5, %1"
+        : "+a"(c0), "+a"(c1)
+        : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
+  } else {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\t"
+        "v_mfma_f32_16x16x32_bf16 %1, %4, %5, %1"
+        : "+a"(c0), "+a"(c1)
+        : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
+  }
+}
+// Wait states between the last MFMA writing AGPR accumulators and any
+// other access to them (the compiler waits 8 after a 16x16x32 bf16 MFMA;
+// 24 here).  Callers pin the accumulators after it ("+a" on an empty asm)
+// so that no read of them is scheduled above it.
+__device__ __forceinline__ void agpr_drain() {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
 }
 
 __device__ __forceinline__ bf16x8 pack_bf16x8(const float* f) {

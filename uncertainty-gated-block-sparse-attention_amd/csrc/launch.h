@@ -26,9 +26,11 @@ constexpr int kStreamBlocksRows = 4096;
 // Largest k_slots the selection kernel sorts (k_max = 112 gives 448).
 constexpr int kMaxSlots = 512;
 
+// elem: the 16-bit element format of the call's tensors (ElemBf16::code 0 or
+// ElemF16::code 1, the C ABI's UGBSA_DTYPE_* values).
 hipError_t launch_block_summary(const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                                int B, int Hk, int N, int D, int mode, uint16_t* planes,
-                                hipStream_t stream);
+                                int B, int Hk, int N, int D, int elem, int mode,
+                                uint16_t* planes, hipStream_t stream);
 
 // Extra modes of the selection kernel.
 //  dump != 0: per-tile order statistics of the unforced tile scores, ranked
@@ -50,8 +52,8 @@ struct SelectAux {
 
 hipError_t launch_select(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                          const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
-                         int mode, float scaling, int k_base, int k_slots, int want_sigma,
-                         int32_t* kv_idx, float* sigma, float* tile_score,
+                         int elem, int mode, float scaling, int k_base, int k_slots,
+                         int want_sigma, int32_t* kv_idx, float* sigma, float* tile_score,
                          hipStream_t stream, const SelectAux* aux = nullptr);
 
 // The v1 per-row selector over a buffer of per-row scores (SelectAux
@@ -78,7 +80,8 @@ hipError_t launch_select_rows(const RowsArgs& a, hipStream_t stream);
 // Per-(b, h) score-noise estimate tau_hat of the score dump.
 hipError_t launch_score_tau(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                             const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
-                            int mode, float scaling, float* tau_hat, hipStream_t stream);
+                            int elem, int mode, float scaling, float* tau_hat,
+                            hipStream_t stream);
 
 hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, int rmode,
                          float tau, int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots,
@@ -102,9 +105,10 @@ hipError_t launch_attn_fwd(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
                            const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                            const uint16_t* vt, const int32_t* kv_idx, int64_t si_b,
                            int64_t si_h, int64_t si_t, int B, int H, int Hk, int M, int N,
-                           int D, int Qt, int k_slots, int block_m, float scale, uint16_t* out,
-                           int64_t so_b, int64_t so_h, int64_t so_m, hipStream_t stream,
-                           const uint64_t* rowmask = nullptr, int32_t* order_ws = nullptr);
+                           int D, int elem, int Qt, int k_slots, int block_m, float scale,
+                           uint16_t* out, int64_t so_b, int64_t so_h, int64_t so_m,
+                           hipStream_t stream, const uint64_t* rowmask = nullptr,
+                           int32_t* order_ws = nullptr);
 
 // The (b, t) tiles of a kv_idx [B, H, Qt, k_slots] ordered by their visited
 // slots over all query heads, heaviest first (64-row tiles): ws holds 2 * B *
@@ -113,9 +117,10 @@ hipError_t launch_attn_tile_order(const int32_t* kv_idx, int64_t si_b, int64_t s
                                   int64_t si_t, int B, int H, int Qt, int k_slots, int NB,
                                   int32_t* ws, hipStream_t stream);
 
-// The pipelined attention kernel at head_dim 256 (attn_fwd256.hip: two
-// 32-row wavefronts per tile, Q in LDS, one K / V^T set per wavefront).
-hipError_t launch_attn_pipe256(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+// The pipelined attention kernel at head_dim 256 (attn_fwd256.hip: one
+// wavefront per 64-row tile, O^T in AGPRs, Q in LDS, one K / V^T set).
+hipError_t launch_attn_pipe256(int elem, const uint16_t* q, int64_t sq_b, int64_t sq_h,
+                               int64_t sq_m,
                                const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
                                const uint16_t* vt, const int32_t* kv_idx,
                                const uint64_t* rowmask, int64_t si_b, int64_t si_h,

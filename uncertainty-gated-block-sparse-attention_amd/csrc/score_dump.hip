@@ -23,7 +23,7 @@ namespace ugbsa {
 constexpr int kTauWaves = 8;
 constexpr int kTauMaxPairs = 1024;   // n_pairs cap of the reference
 
-template <int D, int P, int MT>
+template <typename E, int D, int P, int MT>
 __global__ __launch_bounds__(64 * kTauWaves) void score_tau_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ planes, int Hk, int M, int NB, int grp, int n_pairs,
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(64 * kTauWaves) void score_tau_kernel(
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            acc[mt] = mfma16x16x32(qf[P == 2 ? p : 0][mt][ks], bfr[ks], acc[mt]);
+            acc[mt] = E::mfma(qf[P == 2 ? p : 0][mt][ks], bfr[ks], acc[mt]);
       }
       // rows (4 g4 + 0, 4 g4 + 1) and (4 g4 + 2, 4 g4 + 3) are (lo, hi) of
       // two pairs; dead pairs and blocks past NB score 0 on both rows
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(64 * kTauWaves) void score_tau_kernel(
   }
 }
 
-template <int D, int P>
+template <typename E, int D, int P>
 static hipError_t launch_tau_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                float scaling, float* tau_hat, hipStream_t stream) {
@@ -120,25 +120,38 @@ static hipError_t launch_tau_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, in
   const int NB = (N + kBlock - 1) / kBlock;
   const int n_pairs = M >= 2 ? (M - 1 < kTauMaxPairs ? M - 1 : kTauMaxPairs) : 0;
   const int stride = n_pairs > 0 ? ((M - 1) / n_pairs > 1 ? (M - 1) / n_pairs : 1) : 1;
-  score_tau_kernel<D, P, MT><<<dim3(static_cast<unsigned>(B * H)), 64 * kTauWaves, 0, stream>>>(
+  score_tau_kernel<E, D, P, MT><<<dim3(static_cast<unsigned>(B * H)), 64 * kTauWaves, 0, stream>>>(
       q, sq_b, sq_h, sq_m, planes, Hk, M, NB, H / Hk, n_pairs, stride, scaling, tau_hat);
   return hipGetLastError();
 }
 
-hipError_t launch_score_tau(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
-                            const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
-                            int mode, float scaling, float* tau_hat, hipStream_t stream) {
+template <typename E>
+static hipError_t launch_score_tau_e(const uint16_t* q, int64_t sq_b, int64_t sq_h,
+                                     int64_t sq_m, const uint16_t* planes, int B, int H, int Hk,
+                                     int M, int N, int D, int mode, float scaling,
+                                     float* tau_hat, hipStream_t stream) {
   const bool quest = mode == kModeQuest;
-#define UGBSA_TAU(D_)                                                                       \
-  return quest ? launch_tau_t<D_, 2>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,   \
-                                     tau_hat, stream)                                        \
-               : launch_tau_t<D_, 3>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,   \
-                                     tau_hat, stream)
+#define UGBSA_TAU(D_)                                                                          \
+  return quest ? launch_tau_t<E, D_, 2>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,   \
+                                        tau_hat, stream)                                        \
+               : launch_tau_t<E, D_, 3>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,   \
+                                        tau_hat, stream)
   if (D == 64) UGBSA_TAU(64);
   if (D == 128) UGBSA_TAU(128);
   if (D == 256) UGBSA_TAU(256);
 #undef UGBSA_TAU
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_score_tau(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
+                            const uint16_t* planes, int B, int H, int Hk, int M, int N, int D,
+                            int elem, int mode, float scaling, float* tau_hat,
+                            hipStream_t stream) {
+  if (elem == ElemF16::code)
+    return launch_score_tau_e<ElemF16>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, D, mode,
+                                       scaling, tau_hat, stream);
+  return launch_score_tau_e<ElemBf16>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, D, mode,
+                                      scaling, tau_hat, stream);
 }
 
 }  // namespace ugbsa

@@ -5,17 +5,20 @@
 // copy; the summaries of repeated heads are identical).  Rows past N count as
 // zeros, as F.pad does for the last partial block.
 //
-// Output "planes" [B, Hk, NB, P, D] bf16 is the operand layout of the scoring
-// kernel: P = 2 for Quest (K-max, K-min — exact in bf16) and P = 3 for the
-// mean, stored as an unevaluated sum hi + mid + lo of three bf16 values that
-// reproduces the fp32 mean to within an fp32 rounding, so the bf16 MFMA
-// contraction q . (hi + mid + lo) matches an fp32 q . mean.
+// Output "planes" [B, Hk, NB, P, D] in K's 16-bit format (bf16 or fp16) is
+// the operand layout of the scoring kernel: P = 2 for Quest (K-max, K-min —
+// input values, exact) and P = 3 for the mean, stored as an unevaluated sum
+// hi + mid + lo of three 16-bit values, so the MFMA contraction
+// q . (hi + mid + lo) follows an fp32 q . mean: in bf16 to within an fp32
+// rounding of the mean; in fp16 the lo term can fall in fp16's subnormal
+// range, which bounds the error of the sum by 2^-25 absolute (against
+// 2^-24 relative for an fp32 mean).
 #include "common.h"
 #include "launch.h"
 
 namespace ugbsa {
 
-template <int D>
+template <int D, typename E>
 __global__ __launch_bounds__(256) void block_summary_kernel(
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
     int Hk, int N, int NB, int mode, uint16_t* __restrict__ planes) {
@@ -39,8 +42,8 @@ __global__ __launch_bounds__(256) void block_summary_kernel(
     if (row < N) raw = *reinterpret_cast<const u32x4*>(base + row * sk_n);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float lo = __uint_as_float(raw[j] << 16);
-      const float hi = __uint_as_float(raw[j] & 0xFFFF0000u);
+      const float lo = E::to_f32(raw[j] & 0xFFFFu);
+      const float hi = E::to_f32(raw[j] >> 16);
       s[2 * j] += lo; s[2 * j + 1] += hi;
       mn[2 * j] = fminf(mn[2 * j], lo); mn[2 * j + 1] = fminf(mn[2 * j + 1], hi);
       mx[2 * j] = fmaxf(mx[2 * j], lo); mx[2 * j + 1] = fmaxf(mx[2 * j + 1], hi);
@@ -60,42 +63,51 @@ __global__ __launch_bounds__(256) void block_summary_kernel(
     if (mode == kModeQuest) {
       float a = -INFINITY, z = INFINITY;
       for (int g = 0; g < RG; ++g) { a = fmaxf(a, red[2][g][d]); z = fminf(z, red[1][g][d]); }
-      out[d] = f32_to_bf16(a);          // exact: a bf16 input value (or 0)
-      out[D + d] = f32_to_bf16(z);
+      out[d] = E::from_f32(a);          // exact: an input value (or 0)
+      out[D + d] = E::from_f32(z);
     } else {
       float acc = 0.f;
       for (int g = 0; g < RG; ++g) acc += red[0][g][d];
       const float mean = acc * (1.0f / kBlock);
-      const uint16_t h0 = f32_to_bf16(mean);
-      const float r1 = mean - bf16_to_f32(h0);
-      const uint16_t h1 = f32_to_bf16(r1);
-      const float r2 = r1 - bf16_to_f32(h1);
+      const uint16_t h0 = E::from_f32(mean);
+      const float r1 = mean - E::to_f32(h0);
+      const uint16_t h1 = E::from_f32(r1);
+      const float r2 = r1 - E::to_f32(h1);
       out[d] = h0;
       out[D + d] = h1;
-      out[2 * D + d] = f32_to_bf16(r2);
+      out[2 * D + d] = E::from_f32(r2);
     }
   }
 }
 
-hipError_t launch_block_summary(const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-                                int B, int Hk, int N, int D, int mode, uint16_t* planes,
-                                hipStream_t stream) {
+template <typename E>
+static hipError_t launch_block_summary_e(const uint16_t* k, int64_t sk_b, int64_t sk_h,
+                                         int64_t sk_n, int B, int Hk, int N, int D, int mode,
+                                         uint16_t* planes, hipStream_t stream) {
   const int NB = (N + kBlock - 1) / kBlock;
   dim3 grid(NB, Hk, B);
   switch (D) {
     case 64:
-      block_summary_kernel<64><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
+      block_summary_kernel<64, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
       break;
     case 128:
-      block_summary_kernel<128><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
+      block_summary_kernel<128, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
       break;
     case 256:
-      block_summary_kernel<256><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
+      block_summary_kernel<256, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
       break;
     default:
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_block_summary(const uint16_t* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                                int B, int Hk, int N, int D, int elem, int mode,
+                                uint16_t* planes, hipStream_t stream) {
+  if (elem == ElemF16::code)
+    return launch_block_summary_e<ElemF16>(k, sk_b, sk_h, sk_n, B, Hk, N, D, mode, planes, stream);
+  return launch_block_summary_e<ElemBf16>(k, sk_b, sk_h, sk_n, B, Hk, N, D, mode, planes, stream);
 }
 
 }  // namespace ugbsa

@@ -124,15 +124,16 @@ def record(query, key_states, scaling, block_m=64, sel=None, want_tile_score=Fal
     the reference records nothing: no room for a g_rho gap (rho_k <= k_b) or
     no tile with more than rho_k visible blocks (:152-158).
 
-    ``query`` [B, H, M, D] bf16 on the GPU; ``key_states`` [B, H, N, D]
+    ``query`` [B, H, M, D] bf16 or fp16 on the GPU; ``key_states`` [B, H, N, D]
     (repeat_kv'd) or [B, Hk, N, D].  Synchronises to copy the shard to the
     host, as the reference does.  ``want_tile_score`` adds the unforced
     ``tile_score`` [B, H, Qt, NB] (a tensor) for tests.
     """
     sel = sparse_attention.SEL if sel is None else sel
     assert block_m == BLOCK, "selection tiles are 64 rows"
-    assert query.is_cuda and query.dtype == torch.bfloat16, "bf16 HIP query required"
-    assert key_states.dtype == torch.bfloat16 and key_states.device == query.device
+    assert query.is_cuda, "HIP query required"
+    _capi.dtype_code(query.dtype)                     # bf16 or fp16, as the model runs
+    assert key_states.dtype == query.dtype and key_states.device == query.device
     B, H, M, D = query.shape
     Hk, N = key_states.shape[1], key_states.shape[2]
     assert key_states.shape[0] == B and key_states.shape[3] == D and H % Hk == 0
@@ -155,7 +156,7 @@ def record(query, key_states, scaling, block_m=64, sel=None, want_tile_score=Fal
     tau = torch.empty(B, H, **f32)
     ts = torch.empty(B, H, qt, nb, **f32) if want_tile_score else None
     _capi.check(lib.ugbsa_score_dump(query.data_ptr(), *query.stride(), planes.data_ptr(),
-                                     B, H, Hk, M, N, D, _capi.DTYPE_BF16, mode, float(scaling),
+                                     B, H, Hk, M, N, D, _capi.dtype_code(query.dtype), mode, float(scaling),
                                      k_b, rho_k, g.data_ptr(), r.data_ptr(), sigma.data_ptr(),
                                      g_rho.data_ptr(), valid.data_ptr(), tau.data_ptr(),
                                      _capi.ptr(ts), _capi.stream_ptr(dev)),

@@ -19,10 +19,10 @@ path syncs the host only when ``SEL.log`` asks for diagnostics.
 
 Differences from the reference, by design:
 
-* Scores are fp32 (bf16 inputs, fp32 MFMA accumulation) rather than the model
-  dtype, and ``topk`` ties are broken by block index (the reference leaves the
-  order unspecified).  ``kv_idx`` therefore equals the reference selector run
-  on fp32 scores.
+* Scores are fp32 (bf16 or fp16 inputs — the model's dtype — with fp32 MFMA
+  accumulation) rather than rounded to the model dtype, and ``topk`` ties are
+  broken by block index (the reference leaves the order unspecified).
+  ``kv_idx`` therefore equals the reference selector run on fp32 scores.
 * The dispatcher hands the selector and the kernel the un-repeated
   ``[B, Hk, N, D]`` key/value tensors (GQA handled in-kernel) instead of
   ``repeat_kv`` copies; ``_block_select_kv_idx_v2`` accepts either.
@@ -175,8 +175,9 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
     assert block_m == BLOCK, "selection tiles are 64 rows"
     assert query.shape[-2] == key_states.shape[-2], (
         "query length must equal key length (one-shot prefill: tile t sees blocks <= t)")
-    assert query.is_cuda and query.dtype == torch.bfloat16, "bf16 HIP query required"
-    assert key_states.dtype == torch.bfloat16 and key_states.device == query.device
+    assert query.is_cuda, "HIP query required"
+    _capi.dtype_code(query.dtype)                     # bf16 or fp16, as the model runs
+    assert key_states.dtype == query.dtype and key_states.device == query.device
     B, H, M, D = query.shape
     Hk, N = key_states.shape[1], key_states.shape[2]
     assert key_states.shape[0] == B and key_states.shape[3] == D and H % Hk == 0
@@ -197,7 +198,7 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
     tile_score = (torch.empty(B, H, q_tiles, n_blocks, dtype=torch.float32, device=dev)
                   if want_tile_score else None)
     _capi.check(lib.ugbsa_select(query.data_ptr(), *query.stride(), planes.data_ptr(),
-                                 B, H, Hk, M, N, D, _capi.DTYPE_BF16, mode, float(scaling),
+                                 B, H, Hk, M, N, D, _capi.dtype_code(query.dtype), mode, float(scaling),
                                  k_base, k_slots, block_m, kv_idx.data_ptr(),
                                  _capi.ptr(sigma), _capi.ptr(tile_score), stream),
                 "select")
@@ -218,15 +219,15 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
 
 
 def block_summary(key_states, mode):
-    """Kernel 1: the K-block summary planes [B, Hk, NB, P, D] bf16 of ``mode``
+    """Kernel 1: the K-block summary planes [B, Hk, NB, P, D] (in K's dtype) of ``mode``
     (``_capi.MODE_QUEST`` or ``_capi.MODE_MEAN``), on the current stream."""
     B, Hk, N, D = key_states.shape
     lib = _capi.lib()
     key_states = _contig_rows(key_states)
-    planes = torch.empty(lib.ugbsa_summary_elems(B, Hk, N, D, mode), dtype=torch.bfloat16,
+    planes = torch.empty(lib.ugbsa_summary_elems(B, Hk, N, D, mode), dtype=key_states.dtype,
                          device=key_states.device)
     _capi.check(lib.ugbsa_block_summary(key_states.data_ptr(), *key_states.stride(), B, Hk, N, D,
-                                        _capi.DTYPE_BF16, mode, planes.data_ptr(),
+                                        _capi.dtype_code(key_states.dtype), mode, planes.data_ptr(),
                                         _capi.stream_ptr(key_states.device)),
                 "block summary")
     return planes
@@ -293,8 +294,9 @@ def select_mask_v1(query, key_states, scaling, sel: Selector = None, want_scores
     prefill, as the reference's kernel assumes).
     """
     sel = SEL if sel is None else sel
-    assert query.is_cuda and query.dtype == torch.bfloat16, "bf16 HIP query required"
-    assert key_states.dtype == torch.bfloat16 and key_states.device == query.device
+    assert query.is_cuda, "HIP query required"
+    _capi.dtype_code(query.dtype)                     # bf16 or fp16, as the model runs
+    assert key_states.dtype == query.dtype and key_states.device == query.device
     B, H, M, D = query.shape
     Hk, N = key_states.shape[1], key_states.shape[2]
     assert key_states.shape[0] == B and key_states.shape[3] == D and H % Hk == 0
@@ -327,7 +329,7 @@ def select_mask_v1(query, key_states, scaling, sel: Selector = None, want_scores
     margin = torch.empty(B, H, M, dtype=torch.float32, device=dev) if router else None
     k_eff_kernel = k_eff if (router and nb > 1) else 0
     _capi.check(lib.ugbsa_select_mask(query.data_ptr(), *query.stride(), planes.data_ptr(),
-                                      B, H, Hk, M, N, D, _capi.DTYPE_BF16, mode, float(scaling),
+                                      B, H, Hk, M, N, D, _capi.dtype_code(query.dtype), mode, float(scaling),
                                       _capi.V1_BELIEF if belief else _capi.V1_TOPK, k_bud,
                                       k_eff_kernel, int(sel.k_min), int(sel.k_max),
                                       float(sel.top_p), _capi.ptr(penalty), ws.data_ptr(),
