@@ -349,14 +349,16 @@ def measured_traffic(cfg_name):
 
 
 def attention_kernel_label(D, NB):
-    """The attn_fwd_pipe_kernel<D, NT, QLDS, SB, OA> instance launch_attn_fwd
+    """The attn_fwd_pipe_kernel<E, D, NT, QLDS, SB, OA> instance launch_attn_fwd
     runs for 64-row tiles (csrc/attn_fwd.hip)."""
     if D == 256:
-        return "attn_fwd_pipe_kernel<256, 4, true, true, true>"
-    return f"attn_fwd_pipe_kernel<{D}, 4, false, false, false>"
+        return "attn_fwd_pipe_kernel<ElemBf16, 256, 4, true, true, true>"
+    return f"attn_fwd_pipe_kernel<ElemBf16, {D}, 4, false, false, false>"
 
 
 def roofline(cfg_name, D, NB, tflops):
+    """cfg_name: the workload whose committed traffic summary applies (None
+    when the selector policy differs from the one the summary was taken on)."""
     return {
         "bound": "mfma",
         "kernel": attention_kernel_label(D, NB),
@@ -364,10 +366,10 @@ def roofline(cfg_name, D, NB, tflops):
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-        "traffic": measured_traffic(cfg_name),
+        "traffic": measured_traffic(cfg_name) if cfg_name else None,
         "traffic_source": (traffic_profile(cfg_name) + " (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
                            "calibrated by a 1 GiB copy)"
-                           if measured_traffic(cfg_name) is not None else None),
+                           if cfg_name and measured_traffic(cfg_name) is not None else None),
     }
 
 
@@ -540,7 +542,8 @@ def main():
         },
         "select_mfma_frac": round(runner.select_flops() / (per["select"] * 1e-3) / 1e12
                                   / PEAK_BF16_TFLOPS, 4),
-        "roofline": roofline(cfg.name, cfg.D, runner.NB, attn_tflops),
+        "roofline": roofline(cfg.name if fields == cfg.sel_fields() else None, cfg.D,
+                             runner.NB, attn_tflops),
         "gen_s": round(gen_s, 1),
     }
     if not args.no_dense:

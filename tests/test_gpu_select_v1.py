@@ -275,9 +275,20 @@ class _Module:
 def test_v1_dispatcher_end_to_end(hip_lib, policy):
     """block_sparse_attention with kernel_v2=False: the keep of the GPU
     selector (checked against the oracle) and attention over it."""
-    print(f"[case] v1 dispatcher {policy}", flush=True)
+    check_v1_dispatcher(policy, torch.bfloat16)
+
+
+@pytest.mark.parametrize("policy", ["topk", "router_quest_row_q"])
+def test_v1_dispatcher_end_to_end_fp16(hip_lib, policy):
+    """The per-row path on an fp16 layer: row scores, keep and row-masked
+    attention in fp16."""
+    check_v1_dispatcher(policy, torch.float16)
+
+
+def check_v1_dispatcher(policy, dtype):
+    print(f"[case] v1 dispatcher {policy} {dtype}", flush=True)
     cfg = synth.CONFIGS["c1"]
-    q, k, v = synth.make_layer(cfg, 2, S=2048, dtype=torch.bfloat16)
+    q, k, v = synth.make_layer(cfg, 2, S=2048, dtype=dtype)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     saved = dict(vars(sa.SEL))
     try:
@@ -289,6 +300,7 @@ def test_v1_dispatcher_end_to_end(hip_lib, policy):
         hist0 = None
         out, none = sa.block_sparse_attention(_Module(), qd, kd, vd, None, cfg.scaling)
         assert none is None and out.shape == (1, 2048, 8, 128) and out.is_contiguous()
+        assert out.dtype == dtype
         if policy == "rollout":
             hist1 = sa.SEL.selection_history.clone()
             sa.SEL.selection_history = hist0
