@@ -369,23 +369,33 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
         for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+a"(o[dt][nt]));
     }
   };
-  auto rescale = [&]() {
-    drain_o();
+  // The offset move itself (m, thr, l), leaving the factors for O in alpha.
+  auto move_offsets = [&](float (&alpha)[NT]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const float m_new = fmaxf(m[nt], quad_rows_max(rm[nt]) * sl2);
-      const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_new);
+      alpha[nt] = __builtin_amdgcn_exp2f(m[nt] - m_new);
       m[nt] = m_new;
       thr[nt] = (m_new + kLazyLog2) * inv_sl2;
-      l[nt] *= alpha;
+      l[nt] *= alpha[nt];
+    }
+  };
+  auto scale_o = [&](const float (&alpha)[NT]) {
+    drain_o();
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        o[dt][nt] *= alpha;
+        o[dt][nt] *= alpha[nt];
         // back into its AGPRs at once: left to the allocator, all 256
         // products would stay in VGPRs until the next MFMA reads them
         if constexpr (OA) asm volatile("" : "+a"(o[dt][nt]));
       }
-    }
+  };
+  auto rescale = [&]() {
+    float alpha[NT];
+    move_offsets(alpha);
+    scale_o(alpha);
   };
   // Softmax element e of S (nt = e / 8): P = exp2(S * sl2 - m), the row sum
   // and the bf16 packing of P into pb.
@@ -423,7 +433,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   //   phase 2: O^T += V^T P^T(u) || softmax elements [0, 4 NT) of S(u+1)
   // with the lazy test after phase 1, on the row sums (commit).
   constexpr int NM1 = 2 * NT * KS, P1 = NM1 / 2;
-  constexpr int E1ST = SB ? 0 : 4 * NT;             // first softmax element of phase 1
+  constexpr int E1ST = 4 * NT;                      // first softmax element of phase 1
   constexpr int NE1 = 8 * NT - E1ST;                // softmax elements of phase 1
   constexpr int NM2 = DT * NT, P2 = NM2 / 2;
   constexpr int RU = 4 * NT;                        // row-max units, spread over the P2 pairs
@@ -480,25 +490,46 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       o[dt1][nt1] = E::mfma(vf[dt1], pb[nt1], o[dt1][nt1]);
     }
   };
-  // vn (OA): slabs of the V^T set to load next, each fragment requested
-  // into its registers right after the MFMAs that read it (which gives the
-  // load the rest of this phase and the next phase 1; requesting the K
-  // fragments of phase 1 the same way costs registers the loop does not
-  // have at head_dim 256 and spills, 10 % slower at c5).
-  auto phase2 = [&](const SBuf& nx, VSet& vf, gchar* vn) -> bool {
+  // Phase 2 with SB: O^T += V^T . P^T(u) row set by row set (pairs over the
+  // head dims of one row set, then the next), woven with the lazy test of
+  // S(u+1) over the first row set's pairs and, once it has passed, the
+  // first half of the softmax of S(u+1): row set nt' of P(u+1) is formed
+  // in pb[nt'] once the MFMAs have read row set nt' of P(u).  When some
+  // lane's maxima grew past the lazy bound the offsets move before any of
+  // P(u+1) is formed (m, thr and l at once; O, which the MFMAs of this
+  // phase still accumulate at the old offsets, is scaled by alpha after
+  // the phase).  Returns whether O needs that scaling.
+  auto phase2 = [&](const SBuf& nx, const VSet& vf, float (&alpha)[NT]) -> bool {
+    constexpr int PPN = DT / 2, EPN = 8 / PPN;
+    static_assert(PPN * (NT / 2 + 1) <= P2 && RU % PPN == 0, "phase 2 layout");
     grow = false;
-#pragma unroll
-    for (int j = 0; j < P2; ++j) {
-      pv_pair(vf, j);
+    bool moved = false;
+    static_for<P2>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int nt = (2 * j) / DT, dt0 = (2 * j) % DT;
       if constexpr (OA) {
-        const int dt = (2 * j + 1) / NT;
-        if ((2 * j + 2) % NT == 0) vf[dt] = slab(vn, dt);
+        mfma16x16x32_agpr2<E>(o[dt0][nt], vf[dt0], pb[nt], o[dt0 + 1][nt], vf[dt0 + 1], pb[nt]);
+      } else {
+        o[dt0][nt] = E::mfma(vf[dt0], pb[nt], o[dt0][nt]);
+        o[dt0 + 1][nt] = E::mfma(vf[dt0 + 1], pb[nt], o[dt0 + 1][nt]);
       }
+      if constexpr (j < PPN) {
 #pragma unroll
-      for (int r = (j * RU + P2 - 1) / P2; r < ((j + 1) * RU + P2 - 1) / P2; ++r) rowmax_unit(nx, r);
+        for (int r = j * (RU / PPN); r < (j + 1) * (RU / PPN); ++r) rowmax_unit(nx, r);
+      }
+      if constexpr (j == PPN - 1) {
+        if (__ballot(grow) != 0) {
+          move_offsets(alpha);
+          moved = true;
+        }
+      }
+      if constexpr (j >= PPN && j < PPN * (NT / 2 + 1)) {
+#pragma unroll
+        for (int e = (j - PPN) * EPN; e < (j - PPN + 1) * EPN; ++e) softmax_elem(nx, e);
+      }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    return __ballot(grow) != 0;
+    });
+    return moved;
   };
   auto rowmax = [&](const SBuf& st) -> bool {
     grow = false;
@@ -559,9 +590,9 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   SBuf sa, sb;
   if constexpr (SB) {
     // One K and one V^T set (at head_dim 256 two would take 256 registers).
-    // Step u: S(u) in cur, K(u+1) in ka, V(u) in va; K(u+2) is requested
-    // after phase 1 and V(u+1) after phase 2 — a phase ahead of use (about
-    // 2000 cycles at head_dim 256).
+    // Step u: S(u) in cur (its first half already softmaxed), K(u+1) in ka,
+    // V(u) in va; K(u+2) is requested after phase 1 and V(u+1) after
+    // phase 2 — a phase ahead of use (about 2000 cycles at head_dim 256).
     auto step1 = [&](SBuf& cur, SBuf& nxt, int u) {
       const int rk = blk_raw(u + 2), rm1 = blk_raw(u + 1);
       asm volatile("" : "+v"(lane_b));
@@ -574,9 +605,10 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
         pb[nt] = __builtin_bit_cast(bf16x8, pin);
       }
       mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
-      const bool moved = phase2(nxt, va, v_ptr(uni(rm1), (u + 1) & 1));
-      if constexpr (!OA) load_v(uni(rm1), (u + 1) & 1, va);
-      if (moved) rescale();
+      float alpha[NT];
+      const bool moved = phase2(nxt, va, alpha);
+      load_v(uni(rm1), (u + 1) & 1, va);
+      if (moved) scale_o(alpha);
     };
     if (nv > 0) {
       const int b0 = uni(blk_raw(0));
@@ -588,13 +620,16 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       load_k(uni(blk_raw(1)), clamp_u(1) & 1, ka);
       mask(sa, uni(blk_raw(0)), 0, mbits(0));
       if (rowmax(sa)) rescale();
+#pragma unroll
+      for (int e = 0; e < E1ST; ++e) softmax_elem(sa, e);
       int u = 0;
       for (; u + 2 <= nu - 2; u += 2) {
         step1(sa, sb, u);
         step1(sb, sa, u + 1);
       }
       step1(sa, sb, u);
-      softmax(sb);
+#pragma unroll
+      for (int e = E1ST; e < 8 * NT; ++e) softmax_elem(sb, e);
       pv(va);
     }
   }
