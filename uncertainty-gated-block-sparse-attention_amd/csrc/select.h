@@ -473,32 +473,42 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // B fragments of step s = (p, ks) from LDS, requested one step ahead
+      // of their MFMAs (in program order, so that each step's reads are in
+      // flight behind the previous step's 4 * NT MFMAs instead of waited
+      // for in full before them)
+      auto bload = [&](int s, bf16x8 (&dst)[NT]) {
+        const int p = s / KS, ks = s % KS;
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
+        for (int nt = 0; nt < NT; ++nt)
+          dst[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
+                                                     p * D + 32 * ks + 8 * g4);
+      };
+      bf16x8 bq[2][NT];
+      bload(0, bq[0]);
+      static_for<P * KS>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        constexpr int p = s / KS, ks = s % KS;
+        if constexpr (s + 1 < P * KS) bload(s + 1, bq[(s + 1) & 1]);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          bf16x8 bfr[NT];
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt)
-            bfr[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
-                                                       p * D + 32 * ks + 8 * g4);
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            bf16x8 a;
-            if constexpr (SPLIT_LATE) {
-              // the opaque copy keeps the split inside the chunk loop (hoisted,
-              // both halves would stay live for the whole row)
-              bf16x8 x = qf[0][mt][ks];
-              asm volatile("" : "+v"(x));
-              a = p == 0 ? bf16_pos(x) : bf16_neg(x);
-            } else {
-              a = qf[P == 2 ? p : 0][mt][ks];
-            }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = E::mfma(a, bfr[nt], acc[mt][nt]);
+        for (int mt = 0; mt < 4; ++mt) {
+          bf16x8 a;
+          if constexpr (SPLIT_LATE) {
+            // the opaque copy keeps the split inside the chunk loop (hoisted,
+            // both halves would stay live for the whole row)
+            bf16x8 x = qf[0][mt][ks];
+            asm volatile("" : "+v"(x));
+            a = p == 0 ? bf16_pos(x) : bf16_neg(x);
+          } else {
+            a = qf[P == 2 ? p : 0][mt][ks];
           }
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = E::mfma(a, bq[s & 1][nt], acc[mt][nt]);
         }
-      }
+        // keep each step's reads ahead of the previous step's MFMAs (the
+        // scheduler would otherwise pair two steps' reads and wait on them)
+        __builtin_amdgcn_sched_barrier(0);
+      });
       if constexpr (ROWS) {
         // per-row scores (the v1 selector's input): fl(raw * scaling), -inf
         // past the tile's visible blocks, rows past M skipped
