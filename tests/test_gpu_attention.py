@@ -113,8 +113,10 @@ def test_sparse_gqa_ragged(hip_lib, D, block_m):
     check_close(out, ref, f"D={D} bm={block_m}")
 
 
-@pytest.mark.parametrize("B,Hk", [(1, 1), (1, 2), (1, 3), (2, 2)])
-def test_generations_head_dim_256_every_tile(hip_lib, B, Hk):
+@pytest.mark.parametrize("B,Hk,dtype", [(1, 1, torch.bfloat16), (1, 2, torch.bfloat16),
+                                         (1, 3, torch.bfloat16), (2, 2, torch.bfloat16),
+                                         (1, 2, torch.float16)])
+def test_generations_head_dim_256_every_tile(hip_lib, B, Hk, dtype):
     """Past 512 key blocks the (tile, KV head) units run in generations; at
     head_dim 256 each XCD takes a contiguous run of a generation's tiles when
     Hk divides 8 and the launch holds a multiple of 8 units, and the other
@@ -122,15 +124,15 @@ def test_generations_head_dim_256_every_tile(hip_lib, B, Hk):
     of every head must be written exactly as the oracle computes it: the
     output starts as NaN, 525 blocks with a ragged last tile give a last
     launch of 13 (Hk = 1) or 26 (Hk = 2) units; with B = 2 the tiles of both
-    batch entries share the order."""
-    print(f"[case] generations D=256 B={B} Hk={Hk}", flush=True)
+    batch entries share the order; fp16 runs the same units."""
+    print(f"[case] generations D=256 B={B} Hk={Hk} {dtype}", flush=True)
     H, M, D = 2 * Hk, 33590, 256
-    q, k, v = qkv_small(300 + 10 * B + Hk, B, H, Hk, M, M, D)
+    q, k, v = (x.to(dtype) for x in qkv_small(300 + 10 * B + Hk, B, H, Hk, M, M, D))
     g = torch.Generator().manual_seed(10 * B + Hk)
     nb = (M + 63) // 64
     assert nb > 512
     kv_idx = random_kv_idx(g, B, H, nb, nb, 6)
-    out = torch.full((B, H, M, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    out = torch.full((B, H, M, D), float("nan"), dtype=dtype, device=DEV)
     block_sparse_attn_v2(q.to(DEV), k.to(DEV), v.to(DEV), kv_idx.to(DEV), D ** -0.5, out=out)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
@@ -138,7 +140,7 @@ def test_generations_head_dim_256_every_tile(hip_lib, B, Hk):
     ref = OA.gathered_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
                                 kv_idx.numpy(), D ** -0.5, tiles=tiles, heads=list(range(H)))
     rows = np.concatenate([np.arange(t * 64, min(t * 64 + 64, M)) for t in tiles])
-    check_close(out[:, :, rows], ref[:, :, rows], f"generations B={B} Hk={Hk}")
+    check_close(out[:, :, rows], ref[:, :, rows], f"generations B={B} Hk={Hk} {dtype}")
 
 
 def test_repeated_slot_counts_twice(hip_lib):
