@@ -15,10 +15,12 @@
 //   sigma           (s[k_base-1] - s[k_base]) / max(s[0] - s[k_base], 1e-6) in
 //                   IEEE fp32 (correctly rounded division, denormals kept) (:703-707).
 //
-// Workgroup = one (b, KV head g, Q tile t) and W <= 8 of the group's query
-// heads, one wavefront per head (W chosen by the launcher from the LDS the
-// row needs, so that two or more workgroups share a CU where they fit and
-// one's top-k overlaps another's scoring).  The KV head's summary planes stream through LDS in
+// Workgroup = W <= 8 consecutive (Q tile, query head) pairs of one (b, KV
+// head g), tiles descending, one wavefront per pair (W chosen by the
+// launcher from the LDS the row needs, so that two or more workgroups share
+// a CU where they fit and one's top-k overlaps another's scoring; a
+// workgroup may span two adjacent tiles, since the planes it stages are the
+// KV head's).  The KV head's summary planes stream through LDS in
 // chunks of CH blocks, double-buffered: chunk c + 1 is fetched into
 // registers while chunk c is scored, then stored to the other buffer, one
 // barrier per chunk.  Each wave computes its 64 x CH score chunk on MFMA
@@ -348,7 +350,7 @@ template <typename E, int D, int P, int KP, bool STREAM, bool ROWS>
 __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
     const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
-    int W, int n_hc, float scaling, int k_base, int k_slots, int want_sigma,
+    int W, int wpb, float scaling, int k_base, int k_slots, int want_sigma,
     int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score,
     const SelectAux aux) {
   constexpr int KS = D / 32;
@@ -373,15 +375,23 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   const int g4 = lane >> 4, r16 = lane & 15;
   const int nthreads = blockDim.x;
 
-  const int unit = blockIdx.x / n_hc;
-  const int hc = blockIdx.x % n_hc;
-  const int per_t = B * Hk;
-  const int t = (ROWS ? aux.rows_t1 : Qt) - 1 - unit / per_t;
-  const int b = (unit % per_t) / Hk;
-  const int g = (unit % per_t) % Hk;
-  const int jh = hc * W + wave;
-  const bool active = jh < grp;
-  const int h = g * grp + (active ? jh : 0);
+  // The (tile, query head) pairs of one (b, KV head g), tiles descending,
+  // run W to a workgroup (wpb workgroups per (b, g)), so a workgroup may
+  // take the last heads of tile t and the first of tile t - 1: the planes it
+  // stages are the KV head's, whichever tile reads them.  Workgroup i takes
+  // pair block i / (B Hk) of (b, g) = i % (B Hk): all KV heads' heaviest
+  // tiles first.  Pairs past the end of the range (the last block) idle.
+  const int t_hi = ROWS ? aux.rows_t1 : Qt;
+  const int pairs = (t_hi - (ROWS ? aux.rows_t0 : 0)) * grp;
+  const int bg = blockIdx.x % (B * Hk);
+  const int b = bg / Hk;
+  const int g = bg % Hk;
+  const int p0 = (blockIdx.x / (B * Hk)) * W;       // first pair of the workgroup
+  const bool active = p0 + wave < pairs;
+  const int pw = active ? p0 + wave : p0;
+  const int t = t_hi - 1 - pw / grp;
+  const int h = g * grp + pw % grp;
+  const int t_first = t_hi - 1 - p0 / grp;          // the workgroup's largest tile
   const int H = Hk * grp;
 
   // chunk buffer i at smem + i * chunk_bytes (derived from smem each time, so
@@ -430,7 +440,9 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
 
   const uint16_t* pl = planes + (static_cast<int64_t>(b) * Hk + g) * NB * P * D;
   constexpr int pieces_per_blk = P * D / 8;
-  const int n_chunks = (n_vis + CH - 1) / CH;
+  // chunks up to the workgroup's largest tile (a wave of the next tile
+  // scores one block past its row, which its selection never reads)
+  const int n_chunks = (min(t_first * kBlock + kBlock - 1, N - 1) / kBlock + CH) / CH;
   u32x4 stage[STAGE];
   auto fetch = [&](int c) {
 #pragma unroll
@@ -668,37 +680,37 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   const int grp = H / Hk;
   const SelectLds L = select_lds(P, D, NB, KP, select_chunk(P, D), STREAM);
   constexpr int kLdsMax = 160 * 1024;
-  // W heads per workgroup (ceil(grp / W) workgroups per group): the W that
-  // keeps the most active wavefronts on a CU, given its LDS and at most 8
-  // resident waves (about 230 VGPRs each), counting 10 % more when two or
-  // more workgroups share the CU (one's top-k then overlaps another's
-  // scoring); ties go to the larger W, which stages each plane chunk for
-  // more heads.  W < min(grp, 4) counts half: such workgroups cannot
-  // prefetch a whole chunk into registers (they are only chosen when a long
-  // key range leaves no room in LDS for more heads).
-  int W = 0, n_hc = 0;
+  // W (tile, head) pairs per workgroup, one wavefront each: the W that
+  // keeps the most wavefronts on a CU, given its LDS and at most 8 resident
+  // waves (about 230 VGPRs each), counting 10 % more when two or more
+  // workgroups share the CU (one's top-k then overlaps another's scoring);
+  // ties go to the larger W, which stages each plane chunk for more pairs.
+  // W < 4 counts half: such workgroups cannot prefetch a whole chunk into
+  // registers (they are only chosen when a long key range leaves no room in
+  // LDS for more waves).
+  int W = 0;
   double best = -1.0;
-  for (int w = 1; w <= (grp < kSelWaves ? grp : kSelWaves); ++w) {
+  for (int w = 1; w <= kSelWaves; ++w) {
     const size_t lds_w = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(w) * L.wave_bytes;
     if (lds_w > static_cast<size_t>(kLdsMax)) break;
-    const int hc = (grp + w - 1) / w;
     int per_cu = static_cast<int>(kLdsMax / lds_w);
     if (per_cu > 8 / w) per_cu = 8 / w;
-    const double active = per_cu * static_cast<double>(grp) / hc * (per_cu >= 2 ? 1.1 : 1.0) *
-                          (w < (grp < 4 ? grp : 4) ? 0.5 : 1.0);
-    if (active >= best) { best = active; W = w; n_hc = hc; }
+    const double active = per_cu * static_cast<double>(w) * (per_cu >= 2 ? 1.1 : 1.0) *
+                          (w < 4 ? 0.5 : 1.0);
+    if (active >= best) { best = active; W = w; }
   }
   if (W == 0 || 2 * L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
   const size_t lds = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(W) * L.wave_bytes;
   const int tiles = ROWS ? aux.rows_t1 - aux.rows_t0 : Qt;
-  const int64_t wgs = static_cast<int64_t>(B) * Hk * tiles * n_hc;
+  const int wpb = (tiles * grp + W - 1) / W;        // workgroups per (b, KV head)
+  const int64_t wgs = static_cast<int64_t>(B) * Hk * wpb;
   auto kern = select_kernel<E, D, P, KP, STREAM, ROWS>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds));
   if (e != hipSuccess) return e;
   kern<<<dim3(static_cast<unsigned>(wgs)), 64 * W, lds, stream>>>(
-      q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, n_hc, scaling, k_base,
+      q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, wpb, scaling, k_base,
       k_slots, want_sigma, kv_idx, sigma, tile_score, aux);
   return hipGetLastError();
 }
