@@ -105,3 +105,33 @@ def unexplained_differences(kv_a, kv_b, T_ref, k_base, k_slots, trig_a=None, tri
         if not ok:
             bad.append(r)
     return n_diff, bad
+
+
+def summation_bound(q, k, scaling, quest, fp16_planes=True):
+    """Per (b, h, tile, block): how far two fp32 evaluations of a tile score
+    may differ when they add the same exact products in different orders —
+    2 n 2^-24 (n = P D terms) times the row's sum of |terms|, maxed over the
+    tile's rows — plus, for fp16 mean planes, their lo-term step (2^-25 per
+    element; bf16 planes hold the fp32 mean exactly) and 1e-5.  fp16 x fp16
+    products carry 22 significant bits, bf16 x bf16 16, so with fp16 nearly
+    every fp32 addition rounds; with bf16 large scores do too."""
+    B, H, M, D = q.shape
+    Hk, N = k.shape[1], k.shape[2]
+    grp, nb, qt = H // Hk, (N + 63) // 64, (M + 63) // 64
+    if quest:
+        kmin, kmax = OS.block_summaries(k, True)
+        planes, n = (np.abs(kmax), np.abs(kmin)), 2 * D
+    else:
+        planes, n = (np.abs(OS.block_summaries(k, False)),), 3 * D
+    bound = np.zeros((B, H, qt, nb), np.float64)
+    for b in range(B):
+        for h in range(H):
+            qa = q[b, h].astype(np.float64)
+            if quest:
+                a = np.maximum(qa, 0) @ planes[0][b, h // grp].T - np.minimum(qa, 0) @ planes[1][b, h // grp].T
+            else:
+                a = np.abs(qa) @ planes[0][b, h // grp].T
+            a = np.concatenate([a, np.zeros((qt * 64 - M, nb))]).reshape(qt, 64, nb).max(axis=1)
+            lo = 0.0 if quest or not fp16_planes else D * 2.0 ** -25 * np.abs(qa).max()
+            bound[b, h] = (2 * n * 2.0 ** -24 * a + lo) * abs(scaling) + 1e-5
+    return bound

@@ -27,7 +27,7 @@ import synth
 from block_attn import block_sparse_attn_v2
 from oracle import attention as OA
 from oracle import selector as OS
-from parity import f32np, same_float_bits
+from parity import f32np, same_float_bits, summation_bound
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -125,35 +125,6 @@ def test_select_f16_exact_on_kernel_scores(hip_lib, D, policy):
     assert (np.abs(T_or[fin] - T_k[fin]) <= tol[fin]).all()
     print(f"  max|dT|={np.abs(T_or[fin] - T_k[fin]).max():.2e} (bar {tol[fin].min():.1e}.."
           f"{tol[fin].max():.1e})", flush=True)
-
-
-def summation_bound(q, k, scaling, quest):
-    """Per (b, h, tile, block): how far two fp32 evaluations of a tile score
-    may differ when they add the same exact products in different orders —
-    2 n 2^-24 (n = P D terms) times the row's sum of |terms|, maxed over the
-    tile's rows — plus the mean planes' fp16 lo-term step (2^-25 per element)
-    and 1e-5.  fp16 x fp16 products carry 22 significant bits, so unlike bf16
-    (16) nearly every fp32 addition rounds."""
-    B, H, M, D = q.shape
-    Hk, N = k.shape[1], k.shape[2]
-    grp, nb, qt = H // Hk, (N + 63) // 64, (M + 63) // 64
-    if quest:
-        kmin, kmax = OS.block_summaries(k, True)
-        planes, n = (np.abs(kmax), np.abs(kmin)), 2 * D
-    else:
-        planes, n = (np.abs(OS.block_summaries(k, False)),), 3 * D
-    bound = np.zeros((B, H, qt, nb), np.float64)
-    for b in range(B):
-        for h in range(H):
-            qa = q[b, h].astype(np.float64)
-            if quest:
-                a = np.maximum(qa, 0) @ planes[0][b, h // grp].T - np.minimum(qa, 0) @ planes[1][b, h // grp].T
-            else:
-                a = np.abs(qa) @ planes[0][b, h // grp].T
-            a = np.concatenate([a, np.zeros((qt * 64 - M, nb))]).reshape(qt, 64, nb).max(axis=1)
-            lo = 0.0 if quest else D * 2.0 ** -25 * np.abs(qa).max()
-            bound[b, h] = (2 * n * 2.0 ** -24 * a + lo) * abs(scaling) + 1e-5
-    return bound
 
 
 def random_kv_idx(gen, B, H, qt, nb, slots, block_m=64):

@@ -20,6 +20,7 @@ import torch
 import dump_block_scores as dbs
 import sparse_attention as sa
 import synth
+from parity import summation_bound
 from oracle import score_dump as OD
 from oracle import selector as OS
 
@@ -112,8 +113,7 @@ def test_score_dump_vs_oracle(hip_lib, D, policy):
 def test_score_dump_fp16(hip_lib, D, policy):
     """The dump on an fp16 layer: order statistics bit-identical to the oracle
     on the kernel's own scores; scores within the fp32 summation-order bound
-    of fp16 products (tests/test_gpu_fp16.py); tau_hat within rtol 1e-4."""
-    from test_gpu_fp16 import summation_bound
+    of fp16 products (tests/parity.py); tau_hat within rtol 1e-4."""
     print(f"[case] score_dump fp16 D={D} policy={policy}", flush=True)
     cfg = synth.CONFIGS["c1"]
     q, k, _ = synth.make_layer(cfg, 6, S=2000, D=D, dtype=torch.float16)

@@ -21,7 +21,7 @@ from conftest import load_golden
 from block_attn import block_sparse_attn_v2
 from oracle import attention as OA
 from oracle import selector as OS
-from parity import f32np, same_float_bits, score_gap_tol, unexplained_differences
+from parity import f32np, same_float_bits, score_gap_tol, summation_bound, unexplained_differences
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -118,6 +118,34 @@ def test_select_exact_on_kernel_scores(hip_lib, D, policy):
     fin = np.isfinite(T_or)
     assert np.array_equal(fin, np.isfinite(T_k))
     assert np.abs(T_or[fin] - T_k[fin]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("policy", ["quest", "router_mean_row_q"])
+def test_select_pair_blocks_batch_and_ragged_groups(hip_lib, D, policy):
+    """Select workgroups take consecutive (tile, query head) pairs of one (b,
+    KV head): with B = 2, Hk = 3 and 5 query heads per KV head over 15 tiles
+    (75 pairs per KV head), workgroups span two tiles and the last one of each
+    (b, KV head) holds fewer pairs than waves.  kv_idx and sigma bit-exact on
+    the kernel's own scores; the scores within the fp32 summation-order
+    bound of the oracle's."""
+    print(f"[case] select pair blocks D={D} policy={policy}", flush=True)
+    g = torch.Generator().manual_seed(D)
+    B, H, Hk, S = 2, 15, 3, 900
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hk, S, D, generator=g).to(torch.bfloat16)
+    sel = make_sel(budget_blocks=2, k_min=1, **POLICIES[policy])
+    res, _ = gpu_vs_oracle_on_kernel_scores(q, k, D ** -0.5, sel)
+    quest = OS.SelectorConfig.from_selector(sel).use_quest
+    T_or = OS.tile_scores(q.float().numpy(), k.float().numpy(), D ** -0.5, quest)
+    T_k = res.tile_score.cpu().numpy()
+    fin = np.isfinite(T_or)
+    assert np.array_equal(fin, np.isfinite(T_k))
+    # unit-normal inputs give scores of ~30, where the fp32 summation order
+    # alone moves a score by more than the synthetic layers' 1e-5
+    tol = summation_bound(q.float().numpy(), k.float().numpy(), D ** -0.5, quest,
+                          fp16_planes=False)
+    assert (np.abs(T_or[fin] - T_k[fin]) <= tol[fin]).all()
 
 
 @pytest.mark.parametrize("name", ["a", "b_ragged", "c_full"])
