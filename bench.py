@@ -5,8 +5,9 @@ A step is one sparse prefill attention layer over inputs already resident in
 HBM: K-block summaries -> fused select (scores, tile max, top-k, sigma) ->
 router (quantile, sentinels) -> K/V operand layout -> block-sparse attention.
 ``value`` is ms/layer at BASELINE configs[1] (Qwen2.5-7B-1M layer, 32K,
-router-on-Quest 64 -> 128); the 128K layer and the dense
-comparators are reported in the same line.  Inputs are synthetic (seeded
+router-on-Quest 64 -> 128); the 128K layers (configs[2], 28 of them), one
+head_dim-256 layer and the dense comparators are reported in
+the same line.  Inputs are synthetic (seeded
 N(0,1) with planted needle blocks, synth.py), drawn on the GPU.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
@@ -55,6 +56,8 @@ def parse_args():
                         "backbones, K-mean and Quest, each with and without the router)")
     p.add_argument("--c3-layers", type=int, default=28,
                    help="stacked independent 128K layers for the configs[2] sweep (0 = skip)")
+    p.add_argument("--no-c5", action="store_true",
+                   help="skip the single configs[4] layer (head_dim 256) of the default line")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -592,6 +595,33 @@ def main():
                           "ratio_sparse_vs_dense": round((ms_sweep / args.c3_layers) / best, 4)})
         res["c3"] = c3res
         del layers
+    if not args.no_c5 and args.c3_layers > 0 and args.config != "c5":
+        # one configs[4] layer (head_dim 256, QK-Norm): the workload of the
+        # second attention instance, beside the c3 sweep
+        c5 = synth.CONFIGS["c5"]
+        r5 = LayerRunner(c5, *synth.make_layer_fast(c5, 0, device=dev))
+        torch.cuda.synchronize()
+        ms5, per5 = run_layer_bench(r5, max(3, args.steps // 2), 1, torch)
+        fl5 = r5.attended_flops()
+        ex5 = r5.attended_flops(exact=True)
+        tf5 = fl5 / (per5["attention"] * 1e-3) / 1e12
+        c5res = {"ms_per_layer": round(ms5, 3),
+                 "kernels_ms": {k_: round(v_, 3) for k_, v_ in per5.items()},
+                 "attended_tflop": round(fl5 / 1e12, 3), "attended_tflops": round(tf5, 1),
+                 "causal_exact_tflop": round(ex5 / 1e12, 3),
+                 "causal_exact_tflops": round(ex5 / (per5["attention"] * 1e-3) / 1e12, 1),
+                 "mfma_frac": round(tf5 / PEAK_BF16_TFLOPS, 4),
+                 "roofline": roofline("c5", c5.D, r5.NB, tf5)}
+        if not args.no_dense:
+            sd5, _ = dense_sdpa_ms(r5.q, r5.k, r5.v, c5.scaling, torch, steps=2)
+            k35, k5f = dense_kernel3_ms(r5, torch, steps=2)
+            best = min(x for x in (sd5, k35) if x is not None)
+            c5res.update({"dense_sdpa_ms": None if sd5 is None else round(sd5, 2),
+                          "dense_kernel3_ms": round(k35, 2),
+                          "dense_kernel3_tflops": round(k5f / (k35 * 1e-3) / 1e12, 1),
+                          "ratio_sparse_vs_dense": round(ms5 / best, 4)})
+        res["c5"] = c5res
+        del r5
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, q, k, v, kv_for_cpu, args.cpu_seconds)
     print(json.dumps(res), flush=True)
