@@ -6,8 +6,8 @@ HBM: K-block summaries -> fused select (scores, tile max, top-k, sigma) ->
 router (quantile, sentinels) -> K/V operand layout -> block-sparse attention.
 ``value`` is ms/layer at BASELINE configs[1] (Qwen2.5-7B-1M layer, 32K,
 router-on-Quest 64 -> 128); the 128K layers (configs[2], 28 of them), one
-head_dim-256 layer and the dense comparators are reported in
-the same line.  Inputs are synthetic (seeded
+layer each of configs[3] and configs[4] (head_dim 256) and the dense
+comparators are reported in the same line.  Inputs are synthetic (seeded
 N(0,1) with planted needle blocks, synth.py), drawn on the GPU.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
@@ -57,7 +57,7 @@ def parse_args():
     p.add_argument("--c3-layers", type=int, default=28,
                    help="stacked independent 128K layers for the configs[2] sweep (0 = skip)")
     p.add_argument("--no-c5", action="store_true",
-                   help="skip the single configs[4] layer (head_dim 256) of the default line")
+                   help="skip the single configs[3] and configs[4] layers of the default line")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -376,6 +376,34 @@ def roofline(cfg_name, D, NB, tflops):
     }
 
 
+
+def single_layer_block(cfg, args, torch, synth, dev):
+    """One layer of cfg at its default policy: ms/layer, per-kernel ms,
+    attended TFLOP/s, roofline and the dense ratio."""
+    r = LayerRunner(cfg, *synth.make_layer_fast(cfg, 0, device=dev))
+    torch.cuda.synchronize()
+    ms, per = run_layer_bench(r, max(3, args.steps // 2), 1, torch)
+    fl = r.attended_flops()
+    ex = r.attended_flops(exact=True)
+    tf = fl / (per["attention"] * 1e-3) / 1e12
+    out = {"ms_per_layer": round(ms, 3),
+           "kernels_ms": {k_: round(v_, 3) for k_, v_ in per.items()},
+           "attended_tflop": round(fl / 1e12, 3), "attended_tflops": round(tf, 1),
+           "causal_exact_tflop": round(ex / 1e12, 3),
+           "causal_exact_tflops": round(ex / (per["attention"] * 1e-3) / 1e12, 1),
+           "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
+           "roofline": roofline(cfg.name, cfg.D, r.NB, tf)}
+    if not args.no_dense:
+        sd, _ = dense_sdpa_ms(r.q, r.k, r.v, cfg.scaling, torch, steps=2)
+        k3, k3f = dense_kernel3_ms(r, torch, steps=2)
+        best = min(x for x in (sd, k3) if x is not None)
+        out.update({"dense_sdpa_ms": None if sd is None else round(sd, 2),
+                    "dense_kernel3_ms": round(k3, 2),
+                    "dense_kernel3_tflops": round(k3f / (k3 * 1e-3) / 1e12, 1),
+                    "ratio_sparse_vs_dense": round(ms / best, 4)})
+    del r
+    return out
+
 def pmc_run(cfg, steps, torch, synth, dev):
     q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
     runner = LayerRunner(cfg, q, k, v)
@@ -595,33 +623,12 @@ def main():
                           "ratio_sparse_vs_dense": round((ms_sweep / args.c3_layers) / best, 4)})
         res["c3"] = c3res
         del layers
-    if not args.no_c5 and args.c3_layers > 0 and args.config != "c5":
-        # one configs[4] layer (head_dim 256, QK-Norm): the workload of the
-        # second attention instance, beside the c3 sweep
-        c5 = synth.CONFIGS["c5"]
-        r5 = LayerRunner(c5, *synth.make_layer_fast(c5, 0, device=dev))
-        torch.cuda.synchronize()
-        ms5, per5 = run_layer_bench(r5, max(3, args.steps // 2), 1, torch)
-        fl5 = r5.attended_flops()
-        ex5 = r5.attended_flops(exact=True)
-        tf5 = fl5 / (per5["attention"] * 1e-3) / 1e12
-        c5res = {"ms_per_layer": round(ms5, 3),
-                 "kernels_ms": {k_: round(v_, 3) for k_, v_ in per5.items()},
-                 "attended_tflop": round(fl5 / 1e12, 3), "attended_tflops": round(tf5, 1),
-                 "causal_exact_tflop": round(ex5 / 1e12, 3),
-                 "causal_exact_tflops": round(ex5 / (per5["attention"] * 1e-3) / 1e12, 1),
-                 "mfma_frac": round(tf5 / PEAK_BF16_TFLOPS, 4),
-                 "roofline": roofline("c5", c5.D, r5.NB, tf5)}
-        if not args.no_dense:
-            sd5, _ = dense_sdpa_ms(r5.q, r5.k, r5.v, c5.scaling, torch, steps=2)
-            k35, k5f = dense_kernel3_ms(r5, torch, steps=2)
-            best = min(x for x in (sd5, k35) if x is not None)
-            c5res.update({"dense_sdpa_ms": None if sd5 is None else round(sd5, 2),
-                          "dense_kernel3_ms": round(k35, 2),
-                          "dense_kernel3_tflops": round(k5f / (k35 * 1e-3) / 1e12, 1),
-                          "ratio_sparse_vs_dense": round(ms5 / best, 4)})
-        res["c5"] = c5res
-        del r5
+    if not args.no_c5 and args.c3_layers > 0:
+        # one layer each of configs[3] (its default policy) and configs[4]
+        # (head_dim 256, QK-Norm) beside the c3 sweep
+        for name in ("c4", "c5"):
+            if name != args.config:
+                res[name] = single_layer_block(synth.CONFIGS[name], args, torch, synth, dev)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, q, k, v, kv_for_cpu, args.cpu_seconds)
     print(json.dumps(res), flush=True)
