@@ -113,10 +113,11 @@ def test_sparse_gqa_ragged(hip_lib, D, block_m):
     check_close(out, ref, f"D={D} bm={block_m}")
 
 
-@pytest.mark.parametrize("B,Hk,dtype", [(1, 1, torch.bfloat16), (1, 2, torch.bfloat16),
-                                         (1, 3, torch.bfloat16), (2, 2, torch.bfloat16),
-                                         (1, 2, torch.float16)])
-def test_generations_head_dim_256_every_tile(hip_lib, B, Hk, dtype):
+@pytest.mark.parametrize("B,Hk,dtype,D", [(1, 1, torch.bfloat16, 256), (1, 2, torch.bfloat16, 256),
+                                           (1, 3, torch.bfloat16, 256), (2, 2, torch.bfloat16, 256),
+                                           (1, 2, torch.float16, 256), (1, 2, torch.bfloat16, 128),
+                                           (2, 3, torch.bfloat16, 64)])
+def test_generations_every_tile(hip_lib, B, Hk, dtype, D):
     """Past 512 key blocks the (tile, KV head) units run in generations; at
     head_dim 256 each XCD takes a contiguous run of a generation's tiles when
     Hk divides 8 and the launch holds a multiple of 8 units, and the other
@@ -124,9 +125,10 @@ def test_generations_head_dim_256_every_tile(hip_lib, B, Hk, dtype):
     of every head must be written exactly as the oracle computes it: the
     output starts as NaN, 525 blocks with a ragged last tile give a last
     launch of 13 (Hk = 1) or 26 (Hk = 2) units; with B = 2 the tiles of both
-    batch entries share the order; fp16 runs the same units."""
-    print(f"[case] generations D=256 B={B} Hk={Hk} {dtype}", flush=True)
-    H, M, D = 2 * Hk, 33590, 256
+    batch entries share the order; fp16 runs the same units.  Head_dim 64 /
+    128 deal every launch round robin."""
+    print(f"[case] generations D={D} B={B} Hk={Hk} {dtype}", flush=True)
+    H, M = 2 * Hk, 33590
     q, k, v = (x.to(dtype) for x in qkv_small(300 + 10 * B + Hk, B, H, Hk, M, M, D))
     g = torch.Generator().manual_seed(10 * B + Hk)
     nb = (M + 63) // 64
@@ -140,7 +142,7 @@ def test_generations_head_dim_256_every_tile(hip_lib, B, Hk, dtype):
     ref = OA.gathered_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
                                 kv_idx.numpy(), D ** -0.5, tiles=tiles, heads=list(range(H)))
     rows = np.concatenate([np.arange(t * 64, min(t * 64 + 64, M)) for t in tiles])
-    check_close(out[:, :, rows], ref[:, :, rows], f"generations B={B} Hk={Hk} {dtype}")
+    check_close(out[:, :, rows], ref[:, :, rows], f"generations D={D} B={B} Hk={Hk} {dtype}")
 
 
 def test_repeated_slot_counts_twice(hip_lib):
