@@ -58,6 +58,8 @@ def parse_args():
                    help="stacked independent 128K layers for the configs[2] sweep (0 = skip)")
     p.add_argument("--no-c5", action="store_true",
                    help="skip the single configs[3] and configs[4] layers of the default line")
+    p.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16",
+                   help="element format of Q/K/V (every BASELINE config is bf16)")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -98,15 +100,16 @@ class LayerRunner:
         self.mode = _capi.MODE_QUEST if quest else _capi.MODE_MEAN
         self.router = sel.mode == "router" and self.k_base < self.k_slots
         dev = q.device
+        self.dt = _capi.dtype_code(q.dtype)
         self.planes = torch.empty(self.lib.ugbsa_summary_elems(B, Hk, S, D, self.mode),
-                                  dtype=torch.bfloat16, device=dev)
+                                  dtype=q.dtype, device=dev)
         self.kv_idx = torch.empty(B, H, self.Qt, self.k_slots, dtype=torch.int32, device=dev)
         self.sigma = torch.empty(B, H, self.Qt, dtype=torch.float32, device=dev)
         self.sigma_eff = torch.empty_like(self.sigma)
         self.unc = torch.empty(B, H, self.Qt, dtype=torch.uint8, device=dev)
         self.thr = torch.empty(1, dtype=torch.float32, device=dev)
         self.ws = torch.empty(self.lib.ugbsa_attn_workspace_elems(B, Hk, S, D),
-                              dtype=torch.bfloat16, device=dev)
+                              dtype=q.dtype, device=dev)
         self.out = torch.empty_like(q)
         self.k_quant = max(1, int(float(sel.router_quantile) * B * H * self.Qt))
         self.grain = _capi.GRAIN_ROW if sel.router_grain == "row" else _capi.GRAIN_CELL
@@ -120,11 +123,11 @@ class LayerRunner:
         B, H, Hk, S, D = self.B, self.H, self.Hk, self.S, self.D
         rec = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
         rec(0)
-        c.check(L.ugbsa_block_summary(k.data_ptr(), *k.stride(), B, Hk, S, D, c.DTYPE_BF16,
+        c.check(L.ugbsa_block_summary(k.data_ptr(), *k.stride(), B, Hk, S, D, self.dt,
                                       self.mode, self.planes.data_ptr(), s), "summary")
         rec(1)
         c.check(L.ugbsa_select(q.data_ptr(), *q.stride(), self.planes.data_ptr(), B, H, Hk, S, S, D,
-                               c.DTYPE_BF16, self.mode, float(self.cfg.scaling), self.k_base,
+                               self.dt, self.mode, float(self.cfg.scaling), self.k_base,
                                self.k_slots, 64, self.kv_idx.data_ptr(),
                                self.sigma.data_ptr() if self.router else None, None, s), "select")
         rec(2)
@@ -135,7 +138,7 @@ class LayerRunner:
                                    self.unc.data_ptr(), self.thr.data_ptr(), s), "router")
         rec(3)
         c.check(L.ugbsa_attn_prepare_kv(k.data_ptr(), *k.stride(), v.data_ptr(), *v.stride(),
-                                        B, Hk, S, D, c.DTYPE_BF16, 64, self.ws.data_ptr(), s),
+                                        B, Hk, S, D, self.dt, 64, self.ws.data_ptr(), s),
                 "prepare_kv")
         rec(4)
         self.attention(self.kv_idx)
@@ -146,7 +149,7 @@ class LayerRunner:
         q, k, o = self.q, self.k, self.out
         c.check(L.ugbsa_attn_fwd(q.data_ptr(), *q.stride(), k.data_ptr(), *k.stride(),
                                  None, 0, 0, 0, 1, kv_idx.data_ptr(), *kv_idx.stride(),
-                                 self.B, self.H, self.Hk, self.S, self.S, self.D, c.DTYPE_BF16,
+                                 self.B, self.H, self.Hk, self.S, self.S, self.D, self.dt,
                                  kv_idx.shape[2], kv_idx.shape[3], 64, float(self.cfg.scaling),
                                  o.data_ptr(), *o.stride(), self.ws.data_ptr(), s), "attention")
 
@@ -351,20 +354,23 @@ def measured_traffic(cfg_name):
     return None
 
 
-def attention_kernel_label(D, NB):
+def attention_kernel_label(D, NB, elem="ElemBf16"):
     """The attn_fwd_pipe_kernel<E, D, NT, QLDS, SB, OA> instance launch_attn_fwd
     runs for 64-row tiles (csrc/attn_fwd.hip)."""
     if D == 256:
-        return "attn_fwd_pipe_kernel<ElemBf16, 256, 4, true, true, true>"
-    return f"attn_fwd_pipe_kernel<ElemBf16, {D}, 4, false, false, false>"
+        return f"attn_fwd_pipe_kernel<{elem}, 256, 4, true, true, true>"
+    return f"attn_fwd_pipe_kernel<{elem}, {D}, 4, false, false, false>"
 
 
-def roofline(cfg_name, D, NB, tflops):
+def roofline(cfg_name, D, NB, tflops, fp16=False):
     """cfg_name: the workload whose committed traffic summary applies (None
-    when the selector policy differs from the one the summary was taken on)."""
+    when the selector policy or the element format differs from the ones the
+    summary was taken on: bf16)."""
+    if fp16:
+        cfg_name = None
     return {
         "bound": "mfma",
-        "kernel": attention_kernel_label(D, NB),
+        "kernel": attention_kernel_label(D, NB, "ElemF16" if fp16 else "ElemBf16"),
         "achieved": round(tflops, 1),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
@@ -377,10 +383,15 @@ def roofline(cfg_name, D, NB, tflops):
 
 
 
+def in_dtype(args, torch):
+    """torch dtype of the synthetic Q/K/V (--dtype)."""
+    return torch.float16 if args.dtype == "fp16" else torch.bfloat16
+
+
 def single_layer_block(cfg, args, torch, synth, dev):
     """One layer of cfg at its default policy: ms/layer, per-kernel ms,
     attended TFLOP/s, roofline and the dense ratio."""
-    r = LayerRunner(cfg, *synth.make_layer_fast(cfg, 0, device=dev))
+    r = LayerRunner(cfg, *synth.make_layer_fast(cfg, 0, device=dev, dtype=in_dtype(args, torch)))
     torch.cuda.synchronize()
     ms, per = run_layer_bench(r, max(3, args.steps // 2), 1, torch)
     fl = r.attended_flops()
@@ -392,7 +403,7 @@ def single_layer_block(cfg, args, torch, synth, dev):
            "causal_exact_tflop": round(ex / 1e12, 3),
            "causal_exact_tflops": round(ex / (per["attention"] * 1e-3) / 1e12, 1),
            "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
-           "roofline": roofline(cfg.name, cfg.D, r.NB, tf)}
+           "roofline": roofline(cfg.name, cfg.D, r.NB, tf, args.dtype == "fp16")}
     if not args.no_dense:
         sd, _ = dense_sdpa_ms(r.q, r.k, r.v, cfg.scaling, torch, steps=2)
         k3, k3f = dense_kernel3_ms(r, torch, steps=2)
@@ -404,8 +415,9 @@ def single_layer_block(cfg, args, torch, synth, dev):
     del r
     return out
 
-def pmc_run(cfg, steps, torch, synth, dev):
-    q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
+
+def pmc_run(cfg, steps, torch, synth, dev, dtype):
+    q, k, v = synth.make_layer_fast(cfg, 0, device=dev, dtype=dtype)
     runner = LayerRunner(cfg, q, k, v)
     for _ in range(steps):
         runner.step()
@@ -489,7 +501,7 @@ def run_v1(args, cfg, q, k, v, torch):
         "metric": "v1 per-row sparse prefill ms/layer (kernel_v2=False); executed TFLOP/s",
         "value": round(sel_ms + attn_ms, 4), "unit": "ms/layer", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sel_ms + attn_ms, 4),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": args.dtype,
         "data": "synthetic (seeded N(0,1) Q/K/V with planted needle blocks, synth.make_layer_fast on the GPU)",
         "config": {"workload": f"{cfg.name} shape, v1 {cfg.mode}-on-{cfg.router_score} "
                                f"budget {cfg.budget_blocks} per row, q={cfg.router_quantile} "
@@ -519,10 +531,10 @@ def main():
     torch.cuda.set_device(dev)
     cfg = synth.CONFIGS[args.config]
     if args.pmc_run:
-        pmc_run(cfg, args.steps, torch, synth, dev)
+        pmc_run(cfg, args.steps, torch, synth, dev, in_dtype(args, torch))
         return
     t_gen = time.perf_counter()
-    q, k, v = synth.make_layer_fast(cfg, 0, device=dev)
+    q, k, v = synth.make_layer_fast(cfg, 0, device=dev, dtype=in_dtype(args, torch))
     gen_s = time.perf_counter() - t_gen
     if args.path == "v1":
         print(json.dumps(run_v1(args, cfg, q, k, v, torch)), flush=True)
@@ -552,7 +564,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic (seeded N(0,1) Q/K/V with planted needle blocks, synth.make_layer_fast on the GPU)",
         "config": {"workload": f"{cfg.name}: BASELINE configs[{cfg.index}] — one causal prefill "
                                f"attention layer, B={cfg.B} Hq={cfg.Hq} Hkv={cfg.Hkv} S={cfg.S} "
@@ -574,7 +586,7 @@ def main():
         "select_mfma_frac": round(runner.select_flops() / (per["select"] * 1e-3) / 1e12
                                   / PEAK_BF16_TFLOPS, 4),
         "roofline": roofline(cfg.name if fields == cfg.sel_fields() else None, cfg.D,
-                             runner.NB, attn_tflops),
+                             runner.NB, attn_tflops, args.dtype == "fp16"),
         "gen_s": round(gen_s, 1),
     }
     if not args.no_dense:
@@ -591,7 +603,7 @@ def main():
         c3 = synth.CONFIGS["c3"]
         layers = []
         for layer in range(args.c3_layers):
-            lq, lk, lv = synth.make_layer_fast(c3, layer, device=dev)
+            lq, lk, lv = synth.make_layer_fast(c3, layer, device=dev, dtype=in_dtype(args, torch))
             layers.append(LayerRunner(c3, lq, lk, lv))
         torch.cuda.synchronize()
         sweep_steps = max(1, min(args.steps, 3))
@@ -612,7 +624,7 @@ def main():
                  "causal_exact_tflop": round(ex3 / 1e12, 3),
                  "causal_exact_tflops": round(ex3 / (per3["attention"] * 1e-3) / 1e12, 1),
                  "mfma_frac": round(tf3 / PEAK_BF16_TFLOPS, 4),
-                 "roofline": roofline("c3", c3.D, r0.NB, tf3)}
+                 "roofline": roofline("c3", c3.D, r0.NB, tf3, args.dtype == "fp16")}
         if not args.no_dense:
             sd3, _ = dense_sdpa_ms(r0.q, r0.k, r0.v, c3.scaling, torch, steps=2)
             k33, k3f = dense_kernel3_ms(r0, torch, steps=2)
