@@ -617,7 +617,13 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     wave_lds_sync();
     if (ts != nullptr)
       for (int i = lane; i < NB; i += 64) ts[i] = i < n_vis ? trow[i] : -INFINITY;
-    select_to_cand(trow, n_vis, K, hist, cand, lane, lt_mask);
+    // register keys sized to the row (8, 16 or 32 per lane): the key loops
+    // are unrolled over the slots, so a short row runs far fewer of them
+    // (select at c2 0.175 -> 0.161 ms, c3 1.77 -> 1.72, c4 0.741 -> 0.705;
+    // 4 per lane for rows of up to 256 blocks gains nothing more)
+    if (n_vis <= 64 * 8) select_to_cand<8>(trow, n_vis, K, hist, cand, lane, lt_mask);
+    else if (n_vis <= 64 * 16) select_to_cand<16>(trow, n_vis, K, hist, cand, lane, lt_mask);
+    else select_to_cand<kRegKeys>(trow, n_vis, K, hist, cand, lane, lt_mask);
   }
   wave_lds_sync();
 
