@@ -21,9 +21,10 @@
 // a CU where they fit and one's top-k overlaps another's scoring; a
 // workgroup may span two adjacent tiles, since the planes it stages are the
 // KV head's).  The KV head's summary planes stream through LDS in
-// chunks of CH blocks, double-buffered: chunk c + 1 is fetched into
-// registers while chunk c is scored, then stored to the other buffer, one
-// barrier per chunk.  Each wave computes its 64 x CH score chunk on MFMA
+// chunks of CH blocks: chunk c + 1 is fetched into registers while chunk c
+// is scored, then stored to the other of two buffers (one barrier per
+// chunk), or, where only one buffer leaves room for a second workgroup on
+// the CU, to the same buffer after a second barrier.  Each wave computes its 64 x CH score chunk on MFMA
 // (A = its Q tile, with the Quest sign split done once, from registers;
 // B = planes from LDS), max-pools it over rows in registers and appends CH
 // tile scores to its LDS row.  The row then goes through a 4-pass 8-bit radix
@@ -352,7 +353,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
     int W, int wpb, float scaling, int k_base, int k_slots, int want_sigma,
     int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score,
-    const SelectAux aux) {
+    const SelectAux aux, int nbuf) {
   constexpr int KS = D / 32;
   constexpr int R = KP / 64;
   constexpr int CH = select_chunk(P, D);
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   auto chunk_buf = [&](int i) -> uint16_t* {
     return reinterpret_cast<uint16_t*>(smem + i * L.chunk_bytes);
   };
-  unsigned char* wreg = smem + 2 * L.chunk_bytes + wave * L.wave_bytes;
+  unsigned char* wreg = smem + nbuf * L.chunk_bytes + wave * L.wave_bytes;
   float* trow = reinterpret_cast<float*>(wreg + L.trow_off);
   uint32_t* hist = reinterpret_cast<uint32_t*>(wreg + L.hist_off);
   uint64_t* cand = reinterpret_cast<uint64_t*>(wreg + L.cand_off);
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const bool more = c + 1 < n_chunks;
     if (more) fetch(c + 1);
     if (active) {
-      const uint16_t* chunk = chunk_buf(c & 1);
+      const uint16_t* chunk = chunk_buf(nbuf == 2 ? (c & 1) : 0);
       f32x4 acc[4][NT];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -589,7 +590,8 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
         }
       }
     }
-    if (more) store((c + 1) & 1, c + 1);
+    if (nbuf == 1) __syncthreads();       // every wave is done with the one buffer
+    if (more) store(nbuf == 2 ? ((c + 1) & 1) : 0, c + 1);
     __syncthreads();
   }
   if (!active) return;   // no workgroup barrier follows
@@ -690,23 +692,26 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   // keeps the most wavefronts on a CU, given its LDS and at most 8 resident
   // waves (about 230 VGPRs each), counting 10 % more when two or more
   // workgroups share the CU (one's top-k then overlaps another's scoring);
-  // ties go to the larger W, which stages each plane chunk for more pairs.
-  // W < 4 counts half: such workgroups cannot prefetch a whole chunk into
-  // registers (they are only chosen when a long key range leaves no room in
-  // LDS for more waves).
-  int W = 0;
+  // ties go to the larger W, which stages each plane chunk for more pairs,
+  // and to two chunk buffers over one (one fewer barrier per chunk; one
+  // buffer wins where it alone fits a second workgroup, as at head_dim 256
+  // with three planes: 2.55 -> 2.33 ms at 128K keys).  W < 4 counts half:
+  // such workgroups cannot prefetch a whole chunk into registers (they are
+  // only chosen when a long key range leaves no room in LDS for more waves).
+  int W = 0, nbuf = 2;
   double best = -1.0;
-  for (int w = 1; w <= kSelWaves; ++w) {
-    const size_t lds_w = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(w) * L.wave_bytes;
-    if (lds_w > static_cast<size_t>(kLdsMax)) break;
-    int per_cu = static_cast<int>(kLdsMax / lds_w);
-    if (per_cu > 8 / w) per_cu = 8 / w;
-    const double active = per_cu * static_cast<double>(w) * (per_cu >= 2 ? 1.1 : 1.0) *
-                          (w < 4 ? 0.5 : 1.0);
-    if (active >= best) { best = active; W = w; }
-  }
-  if (W == 0 || 2 * L.chunk_bytes + W * L.wave_bytes > kLdsMax) return hipErrorInvalidConfiguration;
-  const size_t lds = 2 * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(W) * L.wave_bytes;
+  for (int nb = 2; nb >= 1; --nb)
+    for (int w = 1; w <= kSelWaves; ++w) {
+      const size_t lds_w = nb * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(w) * L.wave_bytes;
+      if (lds_w > static_cast<size_t>(kLdsMax)) break;
+      int per_cu = static_cast<int>(kLdsMax / lds_w);
+      if (per_cu > 8 / w) per_cu = 8 / w;
+      const double active = per_cu * static_cast<double>(w) * (per_cu >= 2 ? 1.1 : 1.0) *
+                            (w < 4 ? 0.5 : 1.0);
+      if (active > best || (active == best && nb == nbuf)) { best = active; W = w; nbuf = nb; }
+    }
+  if (W == 0) return hipErrorInvalidConfiguration;
+  const size_t lds = nbuf * static_cast<size_t>(L.chunk_bytes) + static_cast<size_t>(W) * L.wave_bytes;
   const int tiles = ROWS ? aux.rows_t1 - aux.rows_t0 : Qt;
   const int wpb = (tiles * grp + W - 1) / W;        // workgroups per (b, KV head)
   const int64_t wgs = static_cast<int64_t>(B) * Hk * wpb;
@@ -717,7 +722,7 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   if (e != hipSuccess) return e;
   kern<<<dim3(static_cast<unsigned>(wgs)), 64 * W, lds, stream>>>(
       q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, wpb, scaling, k_base,
-      k_slots, want_sigma, kv_idx, sigma, tile_score, aux);
+      k_slots, want_sigma, kv_idx, sigma, tile_score, aux, nbuf);
   return hipGetLastError();
 }
 
