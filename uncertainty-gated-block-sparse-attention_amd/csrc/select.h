@@ -486,10 +486,11 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // B fragments of step s = (p, ks) from LDS, requested one step ahead
+      // B fragments of step s = (p, ks) from LDS, requested two steps ahead
       // of their MFMAs (in program order, so that each step's reads are in
-      // flight behind the previous step's 4 * NT MFMAs instead of waited
-      // for in full before them)
+      // flight behind the two previous steps' 4 * NT MFMAs each instead of
+      // waited for in full before them; one step ahead measured 2-3 %
+      // slower at 128K with Quest planes, the same elsewhere)
       auto bload = [&](int s, bf16x8 (&dst)[NT]) {
         const int p = s / KS, ks = s % KS;
 #pragma unroll
@@ -497,12 +498,13 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
           dst[nt] = *reinterpret_cast<const bf16x8*>(chunk + (16 * nt + r16) * L.row_stride +
                                                      p * D + 32 * ks + 8 * g4);
       };
-      bf16x8 bq[2][NT];
+      bf16x8 bq[3][NT];
       bload(0, bq[0]);
+      if constexpr (P * KS > 1) bload(1, bq[1]);
       static_for<P * KS>([&](auto sc) {
         constexpr int s = decltype(sc)::value;
         constexpr int p = s / KS, ks = s % KS;
-        if constexpr (s + 1 < P * KS) bload(s + 1, bq[(s + 1) & 1]);
+        if constexpr (s + 2 < P * KS) bload(s + 2, bq[(s + 2) % 3]);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
           bf16x8 a;
@@ -516,7 +518,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
             a = qf[P == 2 ? p : 0][mt][ks];
           }
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = E::mfma(a, bq[s & 1][nt], acc[mt][nt]);
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = E::mfma(a, bq[s % 3][nt], acc[mt][nt]);
         }
         // keep each step's reads ahead of the previous step's MFMAs (the
         // scheduler would otherwise pair two steps' reads and wait on them)
