@@ -309,18 +309,19 @@ def test_select_streaming_rows_exact(hip_lib, case):
             assert kv[0] == 0 and kv[1] == nb - 1 and list(kv[2:64]) == list(range(1, 63))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("policy", ["topk", "router_mean_row_q"])
-def test_select_streaming_rows_mean_planes_d256(hip_lib, policy):
+def test_select_streaming_rows_mean_planes_d256(hip_lib, policy, dtype):
     """Streaming rows at head_dim 256 with the three mean planes: a 24 KiB
     plane chunk, which the launcher stages through one chunk buffer (a
     second barrier per chunk) so that two workgroups share a CU.  kv_idx /
     sigma bit-identical to the oracle on the kernel's own scores."""
-    print(f"[case] select streaming D=256 policy={policy}", flush=True)
+    print(f"[case] select streaming D=256 policy={policy} dtype={dtype}", flush=True)
     nb = 4097
     S = nb * 64
     g = torch.Generator().manual_seed(78)
-    q = torch.randn(1, 2, S, 256, generator=g).to(torch.bfloat16)
-    k = torch.randn(1, 1, S, 256, generator=g).to(torch.bfloat16)
+    q = torch.randn(1, 2, S, 256, generator=g).to(dtype)
+    k = torch.randn(1, 1, S, 256, generator=g).to(dtype)
     sel = make_sel(budget_blocks=32, **POLICIES[policy])
     res, _ = gpu_vs_oracle_on_kernel_scores(q, k, 256 ** -0.5, sel)
     assert res.kv_idx.shape[-1] == (128 if policy.startswith("router") else 64)
