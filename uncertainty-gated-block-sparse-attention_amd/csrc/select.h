@@ -347,6 +347,9 @@ __device__ __forceinline__ float sorted_value(const uint64_t (&v)[R], int e, int
 // Blocks per LDS chunk: 32 while a block's planes are at most 512 bytes, else 16.
 __host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 256 ? 32 : 16; }
 
+// W: pairs (waves) per workgroup; wpb: workgroups per (b, KV head); nbuf:
+// plane chunk buffers in LDS, 2 (double-buffered) or 1 (a second barrier
+// per chunk), as the launcher sized the workgroup's LDS.
 template <typename E, int D, int P, int KP, bool STREAM, bool ROWS>
 __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
