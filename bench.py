@@ -138,7 +138,8 @@ class LayerRunner:
                                    self.unc.data_ptr(), self.thr.data_ptr(), s), "router")
         rec(3)
         c.check(L.ugbsa_attn_prepare_kv(k.data_ptr(), *k.stride(), v.data_ptr(), *v.stride(),
-                                        B, Hk, S, D, self.dt, 64, self.ws.data_ptr(), s),
+                                        B, Hk, S, D, self.dt, 64, self.ws.data_ptr(),
+                                        self.ws.numel(), s),
                 "prepare_kv")
         rec(4)
         self.attention(self.kv_idx)
@@ -151,7 +152,8 @@ class LayerRunner:
                                  None, 0, 0, 0, 1, kv_idx.data_ptr(), *kv_idx.stride(),
                                  self.B, self.H, self.Hk, self.S, self.S, self.D, self.dt,
                                  kv_idx.shape[2], kv_idx.shape[3], 64, float(self.cfg.scaling),
-                                 o.data_ptr(), *o.stride(), self.ws.data_ptr(), s), "attention")
+                                 o.data_ptr(), *o.stride(), self.ws.data_ptr(), self.ws.numel(), s),
+                "attention")
 
     def attended_flops(self, kv_idx=None, exact=False) -> float:
         """Attention FLOPs over the visited (tile, block) pairs of kv_idx.
@@ -263,13 +265,21 @@ def dense_kernel3_ms(runner, torch, steps=3):
 
 
 def cpu_model() -> str:
+    """The host CPU's model name, with its family / model / stepping numbers
+    from /proc/cpuinfo (a virtualised host may report a generic name)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, val = (x.strip() for x in line.split(":", 1))
+                info.setdefault(key, val)
+            elif info:
+                break                                   # first processor only
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    ids = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
@@ -278,7 +288,7 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
     head, timed in full when the config is BASELINE configs[0] or [1] (about
     35 s at configs[1]); longer layers stop after budget_s of attention and
     scale by the heads done."""
-    from threadpoolctl import threadpool_info
+    from threadpoolctl import threadpool_info, threadpool_limits
     sys.path.insert(0, ROOT)
     from oracle import attention as OA
     from oracle import selector as OS
@@ -293,6 +303,12 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
     qn = q.float().cpu().numpy()
     kn = k.float().cpu().numpy()
     vn = v.float().cpu().numpy()
+    # BLAS threads: the cores of this process's affinity mask, capped by the
+    # host's per-job thread setting (OMP_NUM_THREADS) where one is given
+    affinity = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    n_threads = min(affinity, int(cap)) if cap.isdigit() and int(cap) > 0 else affinity
+    limits = threadpool_limits(limits=n_threads, user_api="blas")
     t0 = time.perf_counter()
     if full:
         OS.select_kv_idx_v2(qn, kn, cfg.scaling, ocfg)
@@ -313,7 +329,9 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
             break
     att_sample_s = time.perf_counter() - t0
     att_s = att_sample_s / heads_done * cfg.Hq
-    threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    threads = max((p.get("num_threads", 1) for p in threadpool_info()
+                   if p.get("user_api") == "blas"), default=1)
+    limits.restore_original_limits()
     if full:
         sample = (f"numpy fp32 oracle on the whole {cfg.name} layer: v2 selector over all "
                   f"{cfg.Hkv} KV groups ({sel_s:.1f} s) and masked dense attention "
@@ -330,6 +348,8 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
         "cores": int(threads),
         "kind": "port",
         "sample": sample,
+        "affinity_cores": affinity,
+        "blas_threads": int(threads),
         "cpu_model": cpu_model(),
         "select_ms": round(sel_s * 1e3, 1),
         "attention_ms": round(att_s * 1e3, 1),
@@ -337,7 +357,8 @@ def cpu_baseline(cfg, q, k, v, kv_idx, budget_s):
 
 
 def traffic_profile(cfg_name):
-    """The committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of a workload."""
+    """The committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of a workload
+    (a config at its own policy, or "c4_<policy>" for configs[3]'s others)."""
     return os.path.join("profiles", f"attn_fwd_{cfg_name}_traffic.md")
 
 
@@ -352,6 +373,28 @@ def measured_traffic(cfg_name):
     except OSError:
         pass
     return None
+
+
+def policy_key(cfg, fields) -> str | None:
+    """The POLICIES key of a selector field set on cfg (None if none fits)."""
+    for key, pol in POLICIES.items():
+        if all(fields.get(f) == v for f, v in pol.items()) and (
+                pol["mode"] != "router" or fields.get("router_score", "mean") == pol["router_score"]):
+            return key
+    return None
+
+
+def kernel12_rates(runner, per) -> dict:
+    """Achieved HBM GB/s of kernels 1 (summary) and 2 (select) on their
+    algorithmic bytes, with the fraction of the 8 TB/s peak, and kernel 2's
+    scoring MFMA fraction."""
+    b = runner.select_bytes()
+    gbs = {k_: b[k_] / (per[k_] * 1e-3) / 1e9 for k_ in ("summary", "select")}
+    return {"hbm_gbs": {k_: round(v_, 1) for k_, v_ in gbs.items()},
+            "hbm_frac": {k_: round(v_ / PEAK_HBM_GBS, 4) for k_, v_ in gbs.items()},
+            "algorithmic_bytes": b,
+            "select_mfma_frac": round(runner.select_flops() / (per["select"] * 1e-3) / 1e12
+                                      / PEAK_BF16_TFLOPS, 4)}
 
 
 def attention_kernel_label(D, NB, elem="ElemBf16"):
@@ -383,15 +426,30 @@ def roofline(cfg_name, D, NB, tflops, fp16=False):
 
 
 
+def traffic_name(cfg, fields):
+    """The traffic summary that applies to cfg under the selector fields:
+    the config's own ("c4") at its default policy, "c4_<policy>" otherwise."""
+    if fields == cfg.sel_fields():
+        return cfg.name
+    key = policy_key(cfg, fields)
+    return f"{cfg.name}_{key}" if key else None
+
+
 def in_dtype(args, torch):
     """torch dtype of the synthetic Q/K/V (--dtype)."""
     return torch.float16 if args.dtype == "fp16" else torch.bfloat16
 
 
-def single_layer_block(cfg, args, torch, synth, dev):
-    """One layer of cfg at its default policy: ms/layer, per-kernel ms,
-    attended TFLOP/s, roofline and the dense ratio."""
-    r = LayerRunner(cfg, *synth.make_layer_fast(cfg, 0, device=dev, dtype=in_dtype(args, torch)))
+def single_layer_block(cfg, args, torch, synth, dev, policy=None, layer=None, dense=True):
+    """One layer of cfg at its default policy (or POLICIES[policy]): ms/layer,
+    per-kernel ms, attended TFLOP/s, roofline, kernel 1-2 HBM rates and (with
+    dense) the dense ratio.  layer: (q, k, v) already drawn for cfg."""
+    fields = cfg.sel_fields()
+    if policy is not None:
+        fields.update(POLICIES[policy])
+    if layer is None:
+        layer = synth.make_layer_fast(cfg, 0, device=dev, dtype=in_dtype(args, torch))
+    r = LayerRunner(cfg, *layer, sel_fields=fields)
     torch.cuda.synchronize()
     ms, per = run_layer_bench(r, max(3, args.steps // 2), 1, torch)
     fl = r.attended_flops()
@@ -403,8 +461,13 @@ def single_layer_block(cfg, args, torch, synth, dev):
            "causal_exact_tflop": round(ex / 1e12, 3),
            "causal_exact_tflops": round(ex / (per["attention"] * 1e-3) / 1e12, 1),
            "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
-           "roofline": roofline(cfg.name, cfg.D, r.NB, tf, args.dtype == "fp16")}
-    if not args.no_dense:
+           "roofline": roofline(traffic_name(cfg, fields), cfg.D, r.NB, tf,
+                                args.dtype == "fp16"),
+           **kernel12_rates(r, per)}
+    out["policy"] = policy_name(r.sel)
+    if r.router:
+        out["trigger_rate"] = round(float(r.unc.float().mean().item()), 4)
+    if dense and not args.no_dense:
         sd, _ = dense_sdpa_ms(r.q, r.k, r.v, cfg.scaling, torch, steps=2)
         k3, k3f = dense_kernel3_ms(r, torch, steps=2)
         best = min(x for x in (sd, k3) if x is not None)
@@ -550,7 +613,6 @@ def main():
     ms_step, per = run_layer_bench(runner, args.steps, args.warmup, torch)
     attn_flops = runner.attended_flops()
     exact_flops = runner.attended_flops(exact=True)
-    sel_bytes = runner.select_bytes()
     attn_tflops = attn_flops / (per["attention"] * 1e-3) / 1e12
     select_ms = per["summary"] + per["select"] + per["router"]
     res = {
@@ -579,13 +641,8 @@ def main():
         "causal_exact_tflop": round(exact_flops / 1e12, 4),
         "causal_exact_tflops": round(exact_flops / (per["attention"] * 1e-3) / 1e12, 1),
         "trigger_rate": round(float(runner.unc.float().mean().item()), 4) if runner.router else None,
-        "hbm_gbs": {
-            "summary": round(sel_bytes["summary"] / (per["summary"] * 1e-3) / 1e9, 1),
-            "select": round(sel_bytes["select"] / (per["select"] * 1e-3) / 1e9, 1),
-        },
-        "select_mfma_frac": round(runner.select_flops() / (per["select"] * 1e-3) / 1e12
-                                  / PEAK_BF16_TFLOPS, 4),
-        "roofline": roofline(cfg.name if fields == cfg.sel_fields() else None, cfg.D,
+        **kernel12_rates(runner, per),
+        "roofline": roofline(traffic_name(cfg, fields), cfg.D,
                              runner.NB, attn_tflops, args.dtype == "fp16"),
         "gen_s": round(gen_s, 1),
     }
@@ -624,7 +681,8 @@ def main():
                  "causal_exact_tflop": round(ex3 / 1e12, 3),
                  "causal_exact_tflops": round(ex3 / (per3["attention"] * 1e-3) / 1e12, 1),
                  "mfma_frac": round(tf3 / PEAK_BF16_TFLOPS, 4),
-                 "roofline": roofline("c3", c3.D, r0.NB, tf3, args.dtype == "fp16")}
+                 "roofline": roofline("c3", c3.D, r0.NB, tf3, args.dtype == "fp16"),
+                 **kernel12_rates(r0, per3)}
         if not args.no_dense:
             sd3, _ = dense_sdpa_ms(r0.q, r0.k, r0.v, c3.scaling, torch, steps=2)
             k33, k3f = dense_kernel3_ms(r0, torch, steps=2)
@@ -641,6 +699,17 @@ def main():
         for name in ("c4", "c5"):
             if name != args.config:
                 res[name] = single_layer_block(synth.CONFIGS[name], args, torch, synth, dev)
+        if args.config != "c4":
+            # configs[3] runs both backbones, each with and without the router:
+            # the three policies besides its default, on the same layer
+            c4 = synth.CONFIGS["c4"]
+            layer = synth.make_layer_fast(c4, 0, device=dev, dtype=in_dtype(args, torch))
+            default = policy_key(c4, c4.sel_fields())
+            res["c4_policies"] = {
+                key: single_layer_block(c4, args, torch, synth, dev, policy=key, layer=layer,
+                                        dense=False)
+                for key in POLICIES if key != default}
+            del layer
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(cfg, q, k, v, kv_for_cpu, args.cpu_seconds)
     print(json.dumps(res), flush=True)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define UGBSA_ABI_VERSION 2
+#define UGBSA_ABI_VERSION 3
 
 #define UGBSA_OK 0
 #define UGBSA_EARG (-1)     /* bad size / value / null pointer */
@@ -194,21 +194,29 @@ int ugbsa_attn_fwd_rows(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                         int64_t si_h, int64_t si_t, int64_t si_s, int B, int H, int Hk, int M,
                         int N, int D, int dtype, int Qt, int k_slots, int block_m, float scale,
                         void* out, int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d,
-                        void* workspace, void* stream);
+                        void* workspace, int64_t workspace_elems, void* stream);
 
-/* Number of 16-bit elements of the attention workspace: the K and V operand
- * copies of ugbsa_attn_prepare_kv (2 * B * Hk * NB * 64 * D). */
+/* Number of 16-bit elements of the attention workspace, in two parts:
+ *   1. the K and V operand copies written by ugbsa_attn_prepare_kv,
+ *      2 * B * Hk * NB * 64 * D elements (NB = ceil(N / 64));
+ *   2. the tile schedule ugbsa_attn_fwd / ugbsa_attn_fwd_rows write before
+ *      their launches: 2 * B * NB int32 (per-tile work, then the tile order),
+ *      i.e. 4 * B * NB elements rounded up to a multiple of 8 (16 bytes).
+ * ugbsa_attn_prepare_kv needs only part 1; the attention entry points need
+ * both and reject a smaller workspace_elems with UGBSA_EARG. */
 int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D);
 
 /* K and V of every 64-key block re-laid in the attention kernel's operand
  * order (for block_m 64 at head_dim 64/128: K and V^T as 1 KiB per-lane slabs
  * per 32-key half block; otherwise V^T per block), keys past N zero.  Part of
  * block_sparse_attn_v2's work (src/triton_block_attn.py:267-298), exposed so
- * a caller can prepare K/V once and time or reuse it. */
+ * a caller can prepare K/V once and time or reuse it.  workspace_elems: the
+ * 16-bit elements the caller's workspace holds, at least part 1 of
+ * ugbsa_attn_workspace_elems (UGBSA_EARG otherwise). */
 int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                           const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
                           int B, int Hk, int N, int D, int dtype, int block_m, void* workspace,
-                          void* stream);
+                          int64_t workspace_elems, void* stream);
 
 /* Kernel 3 — block-sparse causal attention over kv_idx.
  * Replaces block_sparse_attn_v2 (src/triton_block_attn.py:267-298) and its
@@ -218,7 +226,10 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
  * [B, H, M, D] in dtype (P rounded to dtype before P.V, as the reference's
  * p.to(v.dtype)) with arbitrary strides (head_dim stride 1).  v may be
  * NULL when workspace already holds ugbsa_attn_prepare_kv(k, v, block_m);
- * otherwise the preparation runs first, on the same stream.  scale must be
+ * otherwise the preparation runs first, on the same stream.  workspace holds
+ * workspace_elems 16-bit elements, at least ugbsa_attn_workspace_elems(B, Hk,
+ * N, D): the K/V operand copies, then the tile schedule, which every call
+ * rewrites (UGBSA_EARG before any launch if it is smaller).  scale must be
  * finite and nonzero (UGBSA_EARG otherwise). */
 int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
                    const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
@@ -226,7 +237,8 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
                    const int32_t* kv_idx, int64_t si_b, int64_t si_h, int64_t si_t,
                    int64_t si_s, int B, int H, int Hk, int M, int N, int D, int dtype, int Qt,
                    int k_slots, int block_m, float scale, void* out, int64_t so_b,
-                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace, void* stream);
+                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace,
+                   int64_t workspace_elems, void* stream);
 
 #ifdef __cplusplus
 }

@@ -42,10 +42,11 @@ def visited_blocks(row, t: int, n_blocks: int, block_m: int = 64, block_n: int =
 
 
 def gathered_attention(q, k, v, kv_idx, scale: float, block_m: int = 64,
-                       block_n: int = 64, tiles=None, heads=None):
+                       block_n: int = 64, tiles=None, heads=None, out=None):
     """[B, H, M, D] fp32 output of the v2 kernel semantics.
 
-    ``tiles`` / ``heads`` restrict the work to a subset (rows outside stay 0).
+    ``tiles`` / ``heads`` restrict the work to a subset (rows outside stay 0,
+    or keep what ``out``, a caller's fp32 [B, H, M, D] array, held).
     """
     q, k, v = _f32(q), _f32(k), _f32(v)
     kv = np.asarray(kv_idx)
@@ -53,7 +54,9 @@ def gathered_attention(q, k, v, kv_idx, scale: float, block_m: int = 64,
     Hk, N = k.shape[1], k.shape[2]
     grp = H // Hk
     nb = (N + block_n - 1) // block_n
-    out = np.zeros((B, H, M, D), np.float32)
+    if out is None:
+        out = np.zeros((B, H, M, D), np.float32)
+    assert out.shape == (B, H, M, D) and out.dtype == np.float32
     sc = np.float32(scale)
     tiles = range(kv.shape[2]) if tiles is None else tiles
     heads = range(H) if heads is None else heads
@@ -65,11 +68,13 @@ def gathered_attention(q, k, v, kv_idx, scale: float, block_m: int = 64,
                 if r0 >= M:
                     continue
                 r1 = min(M, r0 + block_m)
-                blks = visited_blocks(kv[b, h, t], t, nb, block_m, block_n)
-                if not blks:
+                blks = np.asarray(visited_blocks(kv[b, h, t], t, nb, block_m, block_n),
+                                  np.int64)
+                if blks.size == 0:
                     continue
-                keys = np.concatenate([np.arange(x * block_n, min(N, x * block_n + block_n))
-                                       for x in blks])
+                # the keys of the visited blocks in slot order, cut at N
+                keys = (blks[:, None] * block_n + np.arange(block_n)).ravel()
+                keys = keys[keys < N]
                 s = (q[b, h, r0:r1] @ k[b, kh, keys].T) * sc
                 rows = np.arange(r0, r1)
                 s[keys[None, :] > rows[:, None]] = -np.inf

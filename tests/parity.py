@@ -135,3 +135,57 @@ def summation_bound(q, k, scaling, quest, fp16_planes=True):
             lo = 0.0 if quest or not fp16_planes else D * 2.0 ** -25 * np.abs(qa).max()
             bound[b, h] = (2 * n * 2.0 ** -24 * a + lo) * abs(scaling) + 1e-5
     return bound
+
+
+# Attention bar of the contract (bf16 inputs, fp32 accumulation).
+ATTN_MAX_ABS, ATTN_MEAN_ABS = 2e-2, 2e-3
+
+
+def oracle_heads(q, k, v, kv_idx, scale, heads, workers=None, chunk=32):
+    """The fp32 oracle's output rows [M, D] of each head in ``heads`` over
+    every tile of ``kv_idx`` (oracle.attention.gathered_attention on the
+    bf16-rounded inputs upcast to fp32).  q [B=1, H, M, D], k / v [1, Hk, N,
+    D] (device or host tensors), kv_idx [1, H, Qt, S].  Tiles are split into
+    chunks of ``chunk`` run on a thread pool (numpy releases the GIL in BLAS
+    and ufuncs), with BLAS held to one thread per worker."""
+    import os
+    import time
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention as OA
+    if workers is None:
+        workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    H, Hk = q.shape[1], k.shape[1]
+    grp = H // Hk
+    kv = kv_idx.cpu().numpy() if torch.is_tensor(kv_idx) else np.asarray(kv_idx)
+    qt = kv.shape[2]
+    res = {}
+    with threadpool_limits(limits=1, user_api="blas"), ThreadPoolExecutor(workers) as ex:
+        for h in heads:
+            t0 = time.perf_counter()
+            g = h // grp
+            qh = f32np(q[:, h:h + 1])
+            kg = f32np(k[:, g:g + 1])
+            vg = f32np(v[:, g:g + 1])
+            kvh = kv[:, h:h + 1]
+            out = np.zeros(qh.shape, np.float32)
+            jobs = [ex.submit(OA.gathered_attention, qh, kg, vg, kvh, scale,
+                              tiles=range(t0_, min(qt, t0_ + chunk)), out=out)
+                    for t0_ in range(0, qt, chunk)]
+            for j in jobs:
+                j.result()
+            res[h] = out[0, 0]
+            print(f"  oracle head {h}: {qt} tiles in {time.perf_counter() - t0:.1f} s", flush=True)
+    return res
+
+
+def check_attention_rows(got, ref, what):
+    """got / ref [M, D] (one head, every row): the contract's max-abs and
+    mean-abs bar; returns (max, mean) of |got - ref|."""
+    err = np.abs(np.asarray(got, np.float32) - np.asarray(ref, np.float32))
+    mx, mn = float(err.max()), float(err.mean())
+    assert np.isfinite(got).all(), f"{what}: non-finite output rows"
+    assert mx <= ATTN_MAX_ABS and mn <= ATTN_MEAN_ABS, (what, mx, mn)
+    return mx, mn

@@ -57,13 +57,13 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"head_dim" in lib.ugbsa_last_error()
     rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 2, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
                             1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
-                            16, 0, 0, 8, 1, 16, None)
+                            16, 0, 0, 8, 1, 16, 1 << 40, None)
     assert rc == -2 and b"stride" in lib.ugbsa_last_error()
     # a zero or non-finite softmax scale is rejected before any launch
     for bad in (0.0, float("inf"), float("nan")):
         rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
                                 1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, bad,
-                                16, 0, 0, 8, 1, 16, None)
+                                16, 0, 0, 8, 1, 16, 1 << 40, None)
         assert rc == -1 and b"scale" in lib.ugbsa_last_error(), bad
     rc = lib.ugbsa_router(16, 1, 8, 4, _capi.GRAIN_ROW, _capi.ROUTER_QUANTILE, 0.1, 0, 16,
                           4, 8, 16, 16, 16, None, None)
@@ -76,8 +76,24 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"query length" in lib.ugbsa_last_error()
     rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
                             1, 8, 2, 64, 128, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
-                            16, 0, 0, 8, 1, 16, None)
+                            16, 0, 0, 8, 1, 16, 1 << 40, None)
     assert rc == -1 and b"query length" in lib.ugbsa_last_error()
+    # a workspace smaller than ugbsa_attn_workspace_elems (K/V copies + tile
+    # schedule) is rejected before any launch, by both attention entry points
+    # and, below the K/V copies, by the preparation
+    need = lib.ugbsa_attn_workspace_elems(1, 2, 64, 128)
+    rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
+                            1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
+                            16, 0, 0, 8, 1, 16, need - 1, None)
+    assert rc == -1 and b"workspace" in lib.ugbsa_last_error()
+    rc = lib.ugbsa_attn_fwd_rows(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 16, 0, 0, 0,
+                                 1, 1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
+                                 16, 0, 0, 8, 1, 16, need - 1, None)
+    assert rc == -1 and b"workspace" in lib.ugbsa_last_error()
+    copies = 2 * 2 * 1 * 64 * 128
+    rc = lib.ugbsa_attn_prepare_kv(16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 1, 2, 64, 128,
+                                   _capi.DTYPE_BF16, 64, 16, copies - 1, None)
+    assert rc == -1 and b"workspace" in lib.ugbsa_last_error()
     # the static-scratch selector refuses shapes whose one-tile pass exceeds its 2^24 fp32
     rc = lib.ugbsa_select_mask_static(16, 0, 0, 8, 1, 16, 1, 128, 2, 4096 * 64, 4096 * 64, 128,
                                       _capi.DTYPE_BF16, _capi.MODE_QUEST, 0.1, _capi.V1_TOPK, 4,

@@ -25,7 +25,11 @@ the way that holds at any size, and on samples where a full check does not fit:
 * sampled tiles: kernel scores within 1e-5 of the oracle's scores from the
   bf16 inputs, kv_idx equal to the oracle's from-scratch selection except
   near ties, and the attention output within max-abs 2e-2 / mean-abs 2e-3 of
-  the fp32 oracle over the kernel's kv_idx.
+  the fp32 oracle over the kernel's kv_idx;
+* the attention of the whole layer under its real launch schedule: an output
+  buffer pre-filled with NaN is finite everywhere afterwards (every row of
+  every head written), and one query head of every KV group matches the fp32
+  oracle on every tile (the oracle run over tile chunks on a thread pool).
 
 Inputs come from ``synth.make_layer_fast`` (seeded, on the device), the same
 generator bench.py times.
@@ -40,7 +44,8 @@ import synth
 from block_attn import block_sparse_attn_v2
 from oracle import attention as OA
 from oracle import selector as OS
-from parity import same_float_bits, score_gap_tol, unexplained_differences
+from parity import (check_attention_rows, oracle_heads, same_float_bits, score_gap_tol,
+                    unexplained_differences)
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -173,3 +178,28 @@ def test_full_config_layer(hip_lib, layers, name, policy):
             err = np.abs(got[0, 0, rows] - ref[0, 0, rows])
             assert err.max() <= 2e-2 and err.mean() <= 2e-3, (h, tt, err.max(), err.mean())
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("name", ["c3", "c4", "c5"])
+def test_full_config_attention_every_tile(hip_lib, layers, name):
+    """The real attention schedule of a full layer (c3: 19 generation
+    launches over 28 heads; c4: 40 heads at 64K; c5: 32 launches, 16 heads,
+    per-XCD tile runs) writes every output row: the buffer starts as NaN and
+    must be finite everywhere after the call.  One query head of every KV
+    group (a different position in each group) is compared with the fp32
+    oracle over the kernel's kv_idx on every tile."""
+    print(f"[case] full config {name}: attention every row / every tile", flush=True)
+    cfg = synth.CONFIGS[name]
+    q, k, v = layers(name)
+    sel = selector_for(cfg, None)
+    grp = cfg.Hq // cfg.Hkv
+    res = sa.select_v2(q, k, cfg.scaling, sel=sel)
+    out = torch.full_like(q, float("nan"))
+    block_sparse_attn_v2(q, k, v, res.kv_idx, cfg.scaling, out=out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all(), "rows left unwritten"
+    heads = [g * grp + g % grp for g in range(cfg.Hkv)]
+    ref = oracle_heads(q, k, v, res.kv_idx, cfg.scaling, heads)
+    for h in heads:
+        mx, mn = check_attention_rows(out[0, h].float().cpu().numpy(), ref[h], f"{name} head {h}")
+        print(f"  {name} head {h}: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)

@@ -135,6 +135,16 @@ def test_v1_select_vs_reference_golden(hip_lib, name):
         for layer in range(layers):
             res = sa.select_mask_v1(qd, kd, scaling, sel=sel, want_scores=True)
             torch.cuda.synchronize()
+            # the kernel's row scores against the reference's (before the
+            # rollout penalty, which the kernel applies inside its ranking):
+            # checked first, so that the cut-tie window below, twice the
+            # measured gap, cannot be widened by a badly wrong row
+            raw = scores[str(rec["scores"]).split("/")[1]]
+            k_sc = res.scores.cpu().numpy()
+            fin = np.isfinite(raw)
+            assert np.array_equal(fin, np.isfinite(k_sc)), f"{pol}: finite pattern"
+            assert (np.abs(raw[fin] - k_sc[fin]) <= 1e-5 * np.maximum(1.0, np.abs(raw[fin]))).all(), \
+                f"{pol}: kernel row scores off the reference's"
             ref_sc = ranked(scores, rec, layer)
             keep_ref = unpack_keep(rec[f"L{layer}/keep_bits"], nb)
             keep = res.keep.cpu().numpy()
@@ -166,7 +176,7 @@ def test_v1_select_vs_reference_golden(hip_lib, name):
                 cut = np.take_along_axis(srt, np.minimum(counts, nb)[..., None] - 1, axis=-1)[..., 0]
                 # within twice the row's measured score gap (at least the
                 # contract's 1e-6 tie window) of the cut
-                tol = score_gap_tol(ref_sc, res.scores.cpu().numpy()).reshape(ref_sc.shape[:-1])
+                tol = score_gap_tol(raw, k_sc).reshape(ref_sc.shape[:-1])
                 with np.errstate(invalid="ignore"):
                     near = np.abs(ref_sc - cut[..., None]) <= tol[..., None]
                 near |= np.isinf(ref_sc) & np.isinf(cut[..., None])

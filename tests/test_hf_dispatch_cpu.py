@@ -100,3 +100,55 @@ def test_launchers_reject_query_shorter_than_keys():
         block_attn.block_sparse_attn(q, k, k, torch.ones(1, 4, 64, 2, dtype=torch.bool), 0.125)
     with pytest.raises(AssertionError, match="query length"):
         sa.select_v2(q, k, 0.125)
+
+
+def test_v1_router_log_line_format(capsys):
+    """The v1 router's per-layer diagnostics go into SEL's three lists, and the
+    last prefill layer prints their running means on the line the reference's
+    harness logs carry (src/sparse_attention.py:355-375)."""
+    from types import SimpleNamespace
+
+    class Model:
+        model = SimpleNamespace(layers=[None, None])
+    saved = dict(vars(sa.SEL))
+    try:
+        sa.SEL.__init__()
+        sa.SEL.log, sa.SEL.model_ref = True, Model()
+        sa.SEL.router_mode, sa.SEL.router_grain, sa.SEL.router_quantile = "quantile", "row", 0.4
+        keep = torch.zeros(1, 2, 4, 8, dtype=torch.bool)
+        keep[..., :3] = True                                   # 3 blocks per cell
+        unc = torch.tensor([[[1, 0, 0, 0], [1, 1, 0, 0]]], dtype=torch.uint8)
+        res = SimpleNamespace(uncertain=unc, margin=torch.full((1, 2, 4), 0.25))
+        sa._log_router_layer(res, keep, 4, 0)                 # not the last layer: no line
+        assert capsys.readouterr().out == ""
+        keep[..., :5] = True                                   # 5 blocks per cell
+        res2 = SimpleNamespace(uncertain=torch.zeros_like(unc), margin=torch.full((1, 2, 4), 0.5))
+        sa._log_router_layer(res2, keep, 4, 1)
+        assert sa.SEL.router_trigger_rate == [0.375, 0.0]
+        assert sa.SEL.router_eff_budget == [3.0, 5.0]
+        assert sa.SEL.router_margin_mean == [0.25, 0.5]
+        assert capsys.readouterr().out == \
+            "  router[quantile/row]: trigger=0.188 eff_budget=4.0 margin=0.375 q=0.40\n"
+        sa.SEL.router_mode, sa.SEL.router_tau = "abs", 0.1
+        sa._log_router_layer(res2, keep, 1, 1)                 # decode (one query row): no line
+        assert capsys.readouterr().out == ""
+        sa._log_router_layer(res2, keep, 4, 1)
+        assert capsys.readouterr().out.endswith(" tau=0.100\n")
+    finally:
+        sa.SEL.__dict__.update(saved)
+
+
+def test_reference_attn_returns_the_inputs_dtype():
+    """reference_attn returns SDPA in the inputs' dtype, as the reference
+    (src/triton_block_attn.py:301-312); reference_attn_fp32 keeps fp32."""
+    from block_attn import reference_attn, reference_attn_fp32
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 130, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    keep = torch.ones(1, 2, 130, 3, dtype=torch.bool)
+    keep[:, :, 70:, 0] = False
+    o = reference_attn(q, k, v, keep, 0.125)
+    o32 = reference_attn_fp32(q, k, v, keep, 0.125)
+    assert o.dtype == torch.bfloat16 and o32.dtype == torch.float32
+    assert torch.equal(o, o32.to(torch.bfloat16))
+    # the causal mask and the keep mask: row 0 sees only key 0
+    assert torch.allclose(o32[:, :, 0], v[:, :, 0].float())

@@ -60,12 +60,3 @@ def test_static_scratch_matches_workspace_path(hip_lib, policy):
         if margin_w is not None:
             assert np.array_equal(margin_s.view(np.uint32), margin_w.view(np.uint32))
 
-
-def test_static_scratch_rejects_oversized_shapes(hip_lib):
-    """B * H * 64 * NB beyond 2^24 fp32: UGBSA_EARG before any launch."""
-    lib = _capi.lib()
-    H, N = 128, 4096 * 64                           # 128 * 64 * 4096 = 2^25
-    rc = lib.ugbsa_select_mask_static(16, 0, 0, 8, 1, 16, 1, H, 2, N, N, 128, _capi.DTYPE_BF16,
-                                      _capi.MODE_QUEST, 0.1, _capi.V1_TOPK, 4, 0, 1, 112, 0.9,
-                                      None, 16, None, None)
-    assert rc == -1 and b"static scratch" in lib.ugbsa_last_error()

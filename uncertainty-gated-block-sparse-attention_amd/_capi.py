@@ -51,18 +51,18 @@ SIGNATURES = {
                                  _p, _i64, _i64, _i64, _i64,
                                  _p, _p, _i64, _i64, _i64, _i64,
                                  _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f,
-                                 _p, _i64, _i64, _i64, _i64, _p, _p]),
+                                 _p, _i64, _i64, _i64, _i64, _p, _i64, _p]),
     "ugbsa_attn_workspace_elems": (_i64, [_i, _i, _i, _i]),
     "ugbsa_attn_prepare_kv": (_i, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64,
-                                   _i, _i, _i, _i, _i, _i, _p, _p]),
+                                   _i, _i, _i, _i, _i, _i, _p, _i64, _p]),
     "ugbsa_attn_fwd": (_i, [_p, _i64, _i64, _i64, _i64,
                             _p, _i64, _i64, _i64, _i64,
                             _p, _i64, _i64, _i64, _i64,
                             _p, _i64, _i64, _i64, _i64,
                             _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f,
-                            _p, _i64, _i64, _i64, _i64, _p, _p]),
+                            _p, _i64, _i64, _i64, _i64, _p, _i64, _p]),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _LIB = None
 

@@ -6,7 +6,8 @@
 HIP attention kernels through the C ABI; ``_compute_kv_idx`` (``:125-146``)
 runs as the HIP kernel ``keep_kv_idx_kernel`` on device tensors (and in torch
 for host tensors, as the reference's kernel test builds ``kv_idx``);
-``reference_attn`` (``:301-312``) forms the SDPA reference.  Differences from
+``reference_attn`` (``:301-312``) forms the SDPA reference in the inputs'
+dtype (``reference_attn_fp32`` keeps it in fp32 for tests).  Differences from
 the reference launchers, all additive:
 
 * K/V may carry ``Hk`` heads with ``H % Hk == 0`` (GQA: query head h reads KV
@@ -85,7 +86,7 @@ def block_sparse_attn_v2(q, k, v, kv_idx, scale, block_n=64, block_m=64,
         v.data_ptr(), *v.stride(),
         kv_idx.data_ptr(), *kv_idx.stride(),
         B, H, Hk, M, N, D, _capi.dtype_code(q.dtype), kv_idx.shape[2], kv_idx.shape[3], block_m,
-        float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(),
+        float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(), workspace.numel(),
         _capi.stream_ptr(q.device))
     _capi.check(rc, "block_sparse_attn_v2")
     return out
@@ -147,7 +148,7 @@ def block_sparse_attn(q, k, v, keep, scale, block_n=64, block_m=64,
         v.data_ptr(), *v.stride(),
         kv.data_ptr(), rm.data_ptr(), *kv.stride(),
         B, H, Hk, M, N, D, _capi.dtype_code(q.dtype), kv.shape[2], max_kept, block_m,
-        float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(),
+        float(scale), out.data_ptr(), *out.stride(), workspace.data_ptr(), workspace.numel(),
         _capi.stream_ptr(q.device))
     _capi.check(rc, "block_sparse_attn")
     return out
@@ -174,11 +175,9 @@ def _compute_kv_idx(keep, block_m):
     return ordered[..., :max_kept].contiguous(), max_kept
 
 
-def reference_attn(q, k, v, keep, scale, block_n=64):
-    """SDPA with the materialised keep-and-causal mask (src/triton_block_attn.py:301-312).
-
-    Runs in fp32 math (inputs upcast) so it is a reference, not a competitor.
-    """
+def reference_attn_fp32(q, k, v, keep, scale, block_n=64):
+    """``reference_attn``'s masked SDPA, computed and returned in fp32
+    (inputs upcast): the tests' reference, kept apart from the drop-in."""
     B, H, M, D = q.shape
     N = k.shape[-2]
     NB = keep.shape[-1]
@@ -192,3 +191,14 @@ def reference_attn(q, k, v, keep, scale, block_n=64):
               <= torch.arange(M, device=q.device).view(M, 1))
     return F.scaled_dot_product_attention(q.float(), k.float(), v.float(),
                                           attn_mask=kk & causal, scale=scale)
+
+
+def reference_attn(q, k, v, keep, scale, block_n=64):
+    """SDPA with the materialised keep-and-causal mask (src/triton_block_attn.py:301-312).
+
+    Returns the inputs' dtype, as the reference's SDPA call does.  The
+    products run in fp32 (inputs upcast, result rounded once): the bf16 SDPA
+    math path issues batched products on transposed views, which this ROCm
+    build has faulted on, and the fp32 form is the closer reference anyway.
+    """
+    return reference_attn_fp32(q, k, v, keep, scale, block_n).to(q.dtype)

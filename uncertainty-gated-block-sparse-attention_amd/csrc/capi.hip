@@ -185,7 +185,7 @@ int ugbsa_router(const float* sigma, int B, int H, int Qt, int grain, int rmode,
 int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                           const void* v, int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t sv_d,
                           int B, int Hk, int N, int D, int dtype, int block_m, void* workspace,
-                          void* stream) {
+                          int64_t workspace_elems, void* stream) {
   int rc = check_dims(B, Hk, Hk, D, dtype);
   if (rc) return rc;
   if ((rc = check_bf16_operand("k", k, sk_b, sk_h, sk_n, sk_d))) return rc;
@@ -193,6 +193,9 @@ int ugbsa_attn_prepare_kv(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_
   if (N < 1) return fail(UGBSA_EARG, "N must be positive");
   if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
   if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace must be a 16-byte aligned buffer");
+  if (workspace_elems < kv_copy_elems(B, Hk, N, D))
+    return fail(UGBSA_EARG, "workspace of %lld elements holds less than the K/V operand copies (%lld)",
+                (long long)workspace_elems, (long long)kv_copy_elems(B, Hk, N, D));
   if (kv_copy_elems(1, 1, N, D) * 2 > 0xFFFFFFFFLL)
     return fail(UGBSA_EARG, "one KV head's K/V copy exceeds 4 GiB (N=%d, D=%d)", N, D);
   return hip_result(ugbsa::launch_attn_prepare(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n,
@@ -315,7 +318,7 @@ int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int
                     int64_t si_t, int64_t si_s, int B, int H, int Hk, int M, int N, int D,
                     int dtype, int Qt, int k_slots, int block_m, float scale, void* out,
                     int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d, void* workspace,
-                    void* stream) {
+                    int64_t workspace_elems, void* stream) {
   int rc = check_dims(B, H, Hk, D, dtype);
   if (rc) return rc;
   if ((rc = check_bf16_operand("q", q, sq_b, sq_h, sq_m, sq_d))) return rc;
@@ -325,8 +328,12 @@ int attn_fwd_common(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int
   if (so_d != 1 || (reinterpret_cast<uintptr_t>(out) & 7u) || so_b % 4 || so_h % 4 || so_m % 4)
     return fail(UGBSA_ELAYOUT, "out: head_dim stride 1, 8-byte aligned rows required");
   if (kv_idx == nullptr || si_s != 1) return fail(UGBSA_ELAYOUT, "kv_idx must be non-null with unit slot stride");
-  if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace (V block transpose) must be a 16-byte aligned buffer");
+  if (workspace == nullptr || !aligned16(workspace)) return fail(UGBSA_EARG, "workspace (K/V operand copies) must be a 16-byte aligned buffer");
   if (M < 1 || N < 1) return fail(UGBSA_EARG, "M and N must be positive");
+  // K/V operand copies, then the tile schedule the launch writes
+  if (workspace_elems < ugbsa_attn_workspace_elems(B, Hk, N, D))
+    return fail(UGBSA_EARG, "workspace of %lld elements is smaller than ugbsa_attn_workspace_elems (%lld)",
+                (long long)workspace_elems, (long long)ugbsa_attn_workspace_elems(B, Hk, N, D));
   // the causal mask takes query row i as key position i (one-shot prefill)
   if (M != N) return fail(UGBSA_EARG, "attention needs query length == key length (M=%d, N=%d)", M, N);
   if (block_m != 64 && block_m != 32) return fail(UGBSA_EARG, "block_m must be 64 or 32 (got %d)", block_m);
@@ -366,11 +373,12 @@ int ugbsa_attn_fwd(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int6
                    const int32_t* kv_idx, int64_t si_b, int64_t si_h, int64_t si_t,
                    int64_t si_s, int B, int H, int Hk, int M, int N, int D, int dtype, int Qt,
                    int k_slots, int block_m, float scale, void* out, int64_t so_b,
-                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace, void* stream) {
+                   int64_t so_h, int64_t so_m, int64_t so_d, void* workspace,
+                   int64_t workspace_elems, void* stream) {
   return attn_fwd_common(q, sq_b, sq_h, sq_m, sq_d, k, sk_b, sk_h, sk_n, sk_d, v, sv_b, sv_h,
                          sv_n, sv_d, kv_idx, nullptr, si_b, si_h, si_t, si_s, B, H, Hk, M, N, D,
                          dtype, Qt, k_slots, block_m, scale, out, so_b, so_h, so_m, so_d,
-                         workspace, stream);
+                         workspace, workspace_elems, stream);
 }
 
 int ugbsa_attn_fwd_rows(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, int64_t sq_d,
@@ -380,12 +388,12 @@ int ugbsa_attn_fwd_rows(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                         int64_t si_h, int64_t si_t, int64_t si_s, int B, int H, int Hk, int M,
                         int N, int D, int dtype, int Qt, int k_slots, int block_m, float scale,
                         void* out, int64_t so_b, int64_t so_h, int64_t so_m, int64_t so_d,
-                        void* workspace, void* stream) {
+                        void* workspace, int64_t workspace_elems, void* stream) {
   if (rowmask == nullptr) return fail(UGBSA_EARG, "rowmask is null");
   return attn_fwd_common(q, sq_b, sq_h, sq_m, sq_d, k, sk_b, sk_h, sk_n, sk_d, v, sv_b, sv_h,
                          sv_n, sv_d, kv_idx, rowmask, si_b, si_h, si_t, si_s, B, H, Hk, M, N, D,
                          dtype, Qt, k_slots, block_m, scale, out, so_b, so_h, so_m, so_d,
-                         workspace, stream);
+                         workspace, workspace_elems, stream);
 }
 
 int ugbsa_keep_kv_idx(const uint8_t* keep, int B, int H, int M, int NB, int block_m,

@@ -379,24 +379,36 @@ def _block_select_mask(query, key_states, scaling, layer_idx):
     """
     res = select_mask_v1(query, key_states, scaling, layer_idx=layer_idx)
     keep = res.keep
-    if SEL.log:
-        if res.uncertain is not None:
-            trig = float(res.uncertain.float().mean().item())
-            SEL.router_trigger_rate.append(trig)
-            SEL.router_eff_budget.append(float(keep.float().sum(dim=-1).mean().item()))
-            SEL.router_margin_mean.append(float(res.margin.mean().item()))
-            n_layers = len(SEL.model_ref.model.layers) if SEL.model_ref is not None else 0
-            if query.shape[-2] > 1 and n_layers and layer_idx == n_layers - 1:
-                tr = sum(SEL.router_trigger_rate) / len(SEL.router_trigger_rate)
-                eb = sum(SEL.router_eff_budget) / len(SEL.router_eff_budget)
-                mg = sum(SEL.router_margin_mean) / len(SEL.router_margin_mean)
-                knob = (f"q={SEL.router_quantile:.2f}" if SEL.router_mode == "quantile"
-                        else f"tau={SEL.router_tau:.3f}")
-                print(f"  router[{SEL.router_mode}/{SEL.router_grain}]: trigger={tr:.3f} "
-                      f"eff_budget={eb:.1f} margin={mg:.3f} {knob}", flush=True)
-        SEL.kept_blocks[layer_idx] = keep[0, :, -1, :].any(dim=0).cpu()
-        SEL.budget_samples.append(keep[0, :, -1, :].sum(dim=-1).float().mean().item())
+    if not SEL.log:
+        return keep
+    if res.uncertain is not None:
+        _log_router_layer(res, keep, query.shape[-2], layer_idx)
+    last_rows = keep[0, :, -1, :]                       # [H, NB], the last query row
+    SEL.kept_blocks[layer_idx] = last_rows.any(dim=0).cpu()
+    SEL.budget_samples.append(last_rows.sum(dim=-1).float().mean().item())
     return keep
+
+
+def _log_router_layer(res, keep, q_len, layer_idx):
+    """One v1 router layer into ``SEL``'s diagnostic lists: the share of
+    triggered cells, the mean kept blocks per cell and the mean margin.  On the
+    last layer of a prefill (``q_len > 1``; layer count from ``SEL.model_ref``)
+    the running means of the three lists are printed on one line, in the
+    format the reference's harness logs parse (src/sparse_attention.py:355-375)."""
+    series = (SEL.router_trigger_rate, SEL.router_eff_budget, SEL.router_margin_mean)
+    values = (res.uncertain.float().mean(), keep.float().sum(dim=-1).mean(), res.margin.mean())
+    for dst, val in zip(series, values):
+        dst.append(float(val.item()))
+    model = SEL.model_ref
+    if q_len <= 1 or model is None or layer_idx != len(model.model.layers) - 1:
+        return
+    trigger, eff_budget, margin = (sum(xs) / len(xs) for xs in series)
+    if SEL.router_mode == "quantile":
+        knob = "q=%.2f" % SEL.router_quantile
+    else:
+        knob = "tau=%.3f" % SEL.router_tau
+    print("  router[%s/%s]: trigger=%.3f eff_budget=%.1f margin=%.3f %s"
+          % (SEL.router_mode, SEL.router_grain, trigger, eff_budget, margin, knob), flush=True)
 
 
 def needle_hit_rate(needle_blocks) -> float:
