@@ -154,7 +154,9 @@ int ugbsa_select_mask(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m, i
  * 64-row tile per pass; larger shapes return UGBSA_EARG before any launch)
  * and calls no allocator.  Every call on a GPU shares that GPU's array, so
  * calls that overlap on one GPU (other streams, other threads) race; the
- * array keeps the last call's scores, and nothing in it needs clearing. */
+ * array keeps the last call's scores, and nothing in it needs clearing.
+ * Under stream capture: make one call on the device first (it looks the
+ * array's address up); a captured call then replays like a direct one. */
 int ugbsa_select_mask_static(const void* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                              int64_t sq_d, const void* planes, int B, int H, int Hk, int M, int N,
                              int D, int dtype, int mode, float scaling, int policy, int k_bud,
