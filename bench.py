@@ -479,9 +479,12 @@ def single_layer_block(cfg, args, torch, synth, dev, policy=None, layer=None, de
     return out
 
 
-def pmc_run(cfg, steps, torch, synth, dev, dtype):
+def pmc_run(cfg, steps, torch, synth, dev, dtype, policy=None):
     q, k, v = synth.make_layer_fast(cfg, 0, device=dev, dtype=dtype)
-    runner = LayerRunner(cfg, q, k, v)
+    fields = cfg.sel_fields()
+    if policy is not None:
+        fields.update(POLICIES[policy])
+    runner = LayerRunner(cfg, q, k, v, sel_fields=fields)
     for _ in range(steps):
         runner.step()
     torch.cuda.synchronize()
@@ -594,7 +597,7 @@ def main():
     torch.cuda.set_device(dev)
     cfg = synth.CONFIGS[args.config]
     if args.pmc_run:
-        pmc_run(cfg, args.steps, torch, synth, dev, in_dtype(args, torch))
+        pmc_run(cfg, args.steps, torch, synth, dev, in_dtype(args, torch), args.policy)
         return
     t_gen = time.perf_counter()
     q, k, v = synth.make_layer_fast(cfg, 0, device=dev, dtype=in_dtype(args, torch))
