@@ -205,3 +205,31 @@ def test_sel_log_diagnostics_and_needle_hit_rate(hip_lib, sel_state, family):
                       for kb in (v.numpy() for v in sa.SEL.kept_blocks.values())])
     assert sa.needle_hit_rate(hit + miss) == pytest.approx(manual)
     assert sa.needle_hit_rate([]) == 1.0
+
+
+@pytest.mark.parametrize("family", sorted(FAMILIES))
+def test_v1_router_log_line_after_install_rollout_hooks(hip_lib, sel_state, family, capsys):
+    """The reference's harnesses call install_rollout_hooks(model) after
+    loading (src/modal_app.py:67); on the v1 path (kernel_v2=False) with
+    SEL.log the router then prints its running means once per prefill, on the
+    model's last decoder layer (src/sparse_attention.py:355-375)."""
+    print(f"[case] hf {family} v1 router log line", flush=True)
+    make_cfg, n_full = FAMILIES[family]
+    sel_policy("router_quest")
+    sa.SEL.kernel_v2 = False
+    sa.SEL.log = True
+    sa.SEL.reset_log()
+    model = build(make_cfg, "block_sparse")
+    sa.install_rollout_hooks(model)
+    capsys.readouterr()
+    with torch.no_grad():
+        model(input_ids(5))
+    torch.cuda.synchronize()
+    lines = [l for l in capsys.readouterr().out.splitlines() if l.startswith("  router[")]
+    assert len(sa.SEL.router_trigger_rate) == n_full
+    mean = lambda xs: sum(xs) / len(xs)
+    want = ("  router[quantile/row]: trigger=%.3f eff_budget=%.1f margin=%.3f q=0.25"
+            % (mean(sa.SEL.router_trigger_rate), mean(sa.SEL.router_eff_budget),
+               mean(sa.SEL.router_margin_mean)))
+    assert lines == [want]
+    assert len(sa.SEL.hidden_at) == len(model.model.layers)

@@ -152,3 +152,34 @@ def test_reference_attn_returns_the_inputs_dtype():
     assert torch.equal(o, o32.to(torch.bfloat16))
     # the causal mask and the keep mask: row 0 sees only key 0
     assert torch.allclose(o32[:, :, 0], v[:, :, 0].float())
+
+
+def test_install_rollout_hooks_sets_model_ref_and_stashes_prefill_inputs():
+    """install_rollout_hooks (src/sparse_attention.py:189-205), which the
+    reference's harnesses call after loading the model: SEL.model_ref is the
+    model and each decoder layer's prefill input lands in SEL.hidden_at;
+    a one-token step leaves the stash alone."""
+    from transformers import AutoModelForCausalLM
+    from transformers.models.qwen2 import Qwen2Config
+    cfg = Qwen2Config(vocab_size=256, hidden_size=64, intermediate_size=128,
+                      num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=2,
+                      max_position_embeddings=512)
+    saved = dict(vars(sa.SEL))
+    try:
+        sa.SEL.__init__()
+        sa.SEL.mode = "dense"
+        torch.manual_seed(0)
+        model = AutoModelForCausalLM.from_config(cfg, attn_implementation="block_sparse").eval()
+        sa.install_rollout_hooks(model)
+        assert sa.SEL.model_ref is model and sa.SEL.hidden_at == {}
+        ids = torch.randint(0, 256, (2, 70), generator=torch.Generator().manual_seed(1))
+        with torch.no_grad():
+            model(ids)
+        assert sorted(sa.SEL.hidden_at) == [0, 1, 2]
+        assert all(h.shape == (2, 70, 64) and not h.requires_grad for h in sa.SEL.hidden_at.values())
+        first = sa.SEL.hidden_at[0]
+        with torch.no_grad():
+            model(ids[:, :1])                       # one query row: not a prefill
+        assert sa.SEL.hidden_at[0] is first
+    finally:
+        sa.SEL.__dict__.update(saved)

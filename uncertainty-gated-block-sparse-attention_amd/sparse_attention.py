@@ -411,6 +411,36 @@ def _log_router_layer(res, keep, q_len, layer_idx):
           % (SEL.router_mode, SEL.router_grain, trigger, eff_budget, margin, knob), flush=True)
 
 
+def install_rollout_hooks(model):
+    """Point ``SEL.model_ref`` at ``model`` and stash every decoder layer's
+    prefill input in ``SEL.hidden_at[layer]`` (src/sparse_attention.py:189-205).
+
+    Harnesses call this right after loading the model.  ``SEL.model_ref`` is
+    what the ``SEL.log`` router summary counts layers from.  The stashed states
+    (a reference to each layer's input tensor, no copy; decode steps with one
+    query row are skipped) feed only ``rollout_peek``, which this build does
+    not provide; they are kept so the call behaves as the reference's, memory
+    included."""
+    SEL.model_ref = model
+    SEL.hidden_at = {}
+    for idx, layer in enumerate(model.model.layers):
+        layer.register_forward_pre_hook(_HiddenStash(idx), with_kwargs=True)
+
+
+class _HiddenStash:
+    """Forward pre-hook of decoder layer ``idx``: its input hidden state of a
+    prefill into ``SEL.hidden_at[idx]``."""
+
+    def __init__(self, idx):
+        self.idx = idx
+
+    def __call__(self, module, args, kwargs):
+        hs = args[0] if args else kwargs.get("hidden_states")
+        if hs is not None and hs.shape[-2] > 1:
+            SEL.hidden_at[self.idx] = hs.detach()
+        return None
+
+
 def needle_hit_rate(needle_blocks) -> float:
     """Mean over logged layers of the fraction of ``needle_blocks`` kept for
     the last Q tile (union over heads), read from ``SEL.kept_blocks`` as the
