@@ -113,6 +113,42 @@ def test_sparse_gqa_ragged(hip_lib, D, block_m):
     check_close(out, ref, f"D={D} bm={block_m}")
 
 
+@pytest.mark.parametrize("D,M", [(64, 700), (128, 700), (256, 700), (128, 33000), (256, 33000)])
+def test_empty_and_sinkless_lists(hip_lib, D, M):
+    """Tiles whose list visits nothing (all sentinels; only blocks past the
+    tile, sentinels and a negative id) get exactly zero rows, as the
+    reference's acc / (l > 0 ? l : 1) does; lists without the sink block
+    (the kernel requests block 0's operands before the list is known and must
+    fetch the real first block instead) match the oracle.  M = 33000 runs the
+    attention in generation launches (more than 512 key blocks)."""
+    print(f"[case] empty / sink-less lists D={D} M={M}", flush=True)
+    B, H, Hk, slots = 1, 4, 2, 6
+    q, k, v = qkv_small(D + M, B, H, Hk, M, M, D)
+    nb = qt = (M + 63) // 64
+    g = torch.Generator().manual_seed(11)
+    kv = random_kv_idx(g, B, H, qt, nb, slots)
+    empty = [0, 5, qt // 2, qt - 1]
+    kv[:, :, empty] = nb                                   # sentinels only
+    kv[:, 1, 5, :3] = torch.tensor([6, nb - 1, -1], dtype=torch.int32)   # invisible / negative
+    sinkless = [2, 3, qt // 3, qt - 2]
+    for t in sinkless:
+        row = torch.full((slots,), nb, dtype=torch.int32)
+        row[0] = t
+        row[1] = max(1, t // 2)
+        kv[:, :, t] = row
+    out = block_sparse_attn_v2(q.to(DEV), k.to(DEV), v.to(DEV), kv.to(DEV), D ** -0.5)
+    torch.cuda.synchronize()
+    got = f32np(out)
+    for t in empty:
+        assert (got[:, :, 64 * t:64 * t + 64] == 0.0).all(), t
+    heads = [0, 1]
+    tiles = sorted(set(empty + sinkless + [1, qt // 4]))
+    ref = OA.gathered_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                kv.numpy(), D ** -0.5, tiles=tiles, heads=heads)
+    rows = np.concatenate([np.arange(64 * t, min(M, 64 * t + 64)) for t in tiles])
+    check_close(out[:, heads][:, :, rows], ref[:, heads][:, :, rows], f"D={D} M={M}")
+
+
 @pytest.mark.parametrize("B,Hk,dtype,D", [(1, 1, torch.bfloat16, 256), (1, 2, torch.bfloat16, 256),
                                            (1, 3, torch.bfloat16, 256), (2, 2, torch.bfloat16, 256),
                                            (1, 2, torch.float16, 256), (1, 2, torch.bfloat16, 128),

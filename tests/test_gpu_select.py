@@ -325,3 +325,33 @@ def test_select_streaming_rows_mean_planes_d256(hip_lib, policy, dtype):
     sel = make_sel(budget_blocks=32, **POLICIES[policy])
     res, _ = gpu_vs_oracle_on_kernel_scores(q, k, 256 ** -0.5, sel)
     assert res.kv_idx.shape[-1] == (128 if policy.startswith("router") else 64)
+
+
+@pytest.mark.parametrize("S", [1, 37, 64, 65, 130, 200])
+@pytest.mark.parametrize("policy", ["topk", "router_quest_row_q", "router_mean_cell_abs"])
+def test_tiny_shapes_select_and_attention(hip_lib, S, policy):
+    """One or a few key blocks (S from 1 token to 4 blocks, ragged): budgets
+    clamp to NB (k_base = k_slots = NB, the router then has nothing to add and
+    is skipped, as the reference's k_base < k_slots test does), selection is
+    bit-exact on the kernel's own scores and the attention over its kv_idx
+    matches the oracle; a single token attends to itself only."""
+    print(f"[case] tiny S={S} policy={policy}", flush=True)
+    g = torch.Generator().manual_seed(S)
+    B, H, Hk, D = 1, 4, 2, 128
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hk, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hk, S, D, generator=g).to(torch.bfloat16)
+    sel = make_sel(budget_blocks=1, k_min=1, **POLICIES[policy])
+    nb = (S + 63) // 64
+    k_base, k_slots = sa.budgets(nb, sel)
+    assert k_base == min(2, nb) and k_slots == (min(2 * k_base, nb) if sel.mode == "router" else k_base)
+    res, _ = gpu_vs_oracle_on_kernel_scores(q, k, D ** -0.5, sel)
+    assert (res.sigma is None) == (k_base == k_slots or sel.mode != "router")
+    kv = res.kv_idx
+    out = block_sparse_attn_v2(q.to(DEV), k.to(DEV), v.to(DEV), kv, D ** -0.5)
+    ref = OA.gathered_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                kv.cpu().numpy(), D ** -0.5)
+    err = np.abs(f32np(out) - ref)
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+    if S == 1:
+        assert torch.equal(out[0, :, 0].cpu(), v[0].repeat_interleave(H // Hk, dim=0)[:, 0])
