@@ -259,6 +259,17 @@ __device__ __forceinline__ float quad_rows_max(float v) {
   auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+// quad_rows_max with v_med3_f32(a, b, bound): bound = +inf gives max(a, b),
+// -inf min(a, b), without the canonicalising copy IEEE mode puts before each
+// fmaxf / fminf of an MFMA result.  bound must sit in a register the
+// optimiser cannot see through (an empty asm on it), or the med3 folds back
+// into fmaxf / fminf.
+__device__ __forceinline__ float quad_rows_med3(float v, float bound) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __builtin_amdgcn_fmed3f(__uint_as_float(a[0]), __uint_as_float(a[1]), bound);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __builtin_amdgcn_fmed3f(__uint_as_float(b[0]), __uint_as_float(b[1]), bound);
+}
 __device__ __forceinline__ float quad_rows_sum(float v) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);

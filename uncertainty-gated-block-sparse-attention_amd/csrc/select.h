@@ -448,16 +448,27 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   // scores one block past its row, which its selection never reads)
   const int n_chunks = (min(t_first * kBlock + kBlock - 1, N - 1) / kBlock + CH) / CH;
   u32x4 stage[STAGE];
-  auto fetch = [&](int c) {
+  // A chunk's blocks are contiguous, so piece pi of any chunk sits at byte
+  // 16 pi from the chunk's start: each thread's offsets are fixed.  Pieces
+  // past PIECES (a workgroup with more threads than a stage needs) get an
+  // offset beyond every range.
+  uint32_t voff[STAGE];
 #pragma unroll
-    for (int j = 0; j < STAGE; ++j) {
-      const int pi = threadIdx.x + j * nthreads;
-      const int bl = pi / pieces_per_blk, off = pi % pieces_per_blk;
-      const int blk = c * CH + bl;
-      stage[j] = u32x4{0u, 0u, 0u, 0u};
-      if (pi < PIECES && blk < NB)
-        stage[j] = *reinterpret_cast<const u32x4*>(pl + static_cast<int64_t>(blk) * P * D + off * 8);
-    }
+  for (int j = 0; j < STAGE; ++j) {
+    const int pi = threadIdx.x + j * nthreads;
+    voff[j] = pi < PIECES ? 16u * static_cast<uint32_t>(pi) : 0x80000000u;
+  }
+  // Chunk c through a buffer resource from the chunk's first block to block
+  // NB: pieces past the last block read zeros (the F.pad rows of the
+  // reference's summaries never reach a score), with no branch or clearing.
+  auto fetch = [&](int c) {
+    const int left = NB - c * CH;                     // >= 1 for every chunk fetched
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(pl + static_cast<int64_t>(c) * CH * P * D,
+                  static_cast<uint32_t>(left) * (P * D * 2));
+#pragma unroll
+    for (int j = 0; j < STAGE; ++j)
+      stage[j] = __builtin_bit_cast(u32x4, buffer_load_bf16x8(rs, voff[j], 0u));
   };
   auto store = [&](int buf, int c) {
 #pragma unroll
@@ -475,6 +486,9 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     }
   };
   const bool pos_scale = scaling >= 0.f;
+  // +inf in a register the optimiser cannot see through (tile max-pool)
+  float pinf = INFINITY;
+  asm volatile("" : "+v"(pinf));
 
   fetch(0);
   store(0, 0);
@@ -548,22 +562,17 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
         // tile max over the 64 rows of (score * scaling): the max (min for a
         // negative scaling) of the raw sums, scaled once — fl(x * s) is
         // monotone in x, so this is the max of the scaled scores exactly.
+        // (v_med3 with an opaque +-inf bound: max / min without the
+        // canonicalising copies fmaxf / fminf of MFMA results get)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
+          const float bound = pos_scale ? pinf : -pinf;
           float mx = acc[0][nt][0];
-          if (pos_scale) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
+          for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-              for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[mt][nt][i]);
-            mx = quad_rows_max(mx);
-          } else {
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) mx = fminf(mx, acc[mt][nt][i]);
-            mx = -quad_rows_max(-mx);
-          }
+            for (int i = 0; i < 4; ++i) mx = __builtin_amdgcn_fmed3f(mx, acc[mt][nt][i], bound);
+          mx = quad_rows_med3(mx, bound);
           const int blk = c * CH + 16 * nt + r16;
           if (g4 == nt % 4 && blk < NB) trow[STREAM ? 16 * nt + r16 : blk] = mx * scaling;
         }
