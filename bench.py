@@ -174,8 +174,7 @@ class LayerRunner:
     def select_bytes(self) -> dict:
         """Algorithmic HBM bytes of kernels 1 and 2 (one launch each)."""
         B, H, Hk, S, D, NB = self.B, self.H, self.Hk, self.S, self.D, self.NB
-        P = 2 if self.mode == self.capi.MODE_QUEST else 3
-        planes = B * Hk * NB * P * D * 2
+        planes = self.lib.ugbsa_summary_elems(B, Hk, S, D, self.mode) * 2
         k1 = B * Hk * S * D * 2 + planes
         k2 = B * H * S * D * 2 + planes + B * H * self.Qt * self.k_slots * 4 + B * H * self.Qt * 4
         return {"summary": k1, "select": k2}

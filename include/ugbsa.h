@@ -11,7 +11,8 @@
  *  - Pointers are device pointers (e.g. torch.Tensor.data_ptr()); the library
  *    never allocates or frees device memory and keeps no pointer after return.
  *  - Strides are in elements (int64).  The 16-bit tensors of a call (q, k, v,
- *    the summary planes, out) share one element format, `dtype`:
+ *    the Quest summary planes, out) share one element format, `dtype`
+ *    (the mean summary is fp16 and fp32 for both, see ugbsa_block_summary):
  *    UGBSA_DTYPE_BF16 or UGBSA_DTYPE_F16 — the reference runs in the model's
  *    dtype (src/triton_block_attn.py:267-298, src/sparse_attention.py:588-748).
  *    They need head_dim stride 1, 16-byte aligned base pointers and other
@@ -32,7 +33,7 @@
 extern "C" {
 #endif
 
-#define UGBSA_ABI_VERSION 3
+#define UGBSA_ABI_VERSION 4
 
 #define UGBSA_OK 0
 #define UGBSA_EARG (-1)     /* bad size / value / null pointer */
@@ -56,15 +57,19 @@ extern "C" {
 int ugbsa_abi_version(void);
 const char* ugbsa_last_error(void);
 
-/* Number of 16-bit elements of the block-summary buffer [B, Hk, NB, P, D]
- * (P = 2 for Quest, 3 for mean). */
+/* Number of 16-bit elements of the block-summary buffer: Quest
+ * [B, Hk, NB, 2, D]; mean [B, Hk, NB, 2, D] fp16 followed by [B, Hk, NB] fp32
+ * (B * Hk * NB * (2 * D + 2) in all). */
 int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode);
 
 /* Kernel 1 — per-64-token-block K summaries of k [B, Hk, N, D] (dtype).
  * Replaces the summary step of _block_select_kv_idx_v2:
  * src/sparse_attention.py:618-622 (zero pad), :636-637 (amin/amax, Quest),
- * :646 (mean).  Output planes, in dtype: Quest (K-max, K-min), mean (hi, mid,
- * lo terms of the fp32 mean). */
+ * :646 (mean).  Output: Quest, two planes in dtype (K-max, K-min, exact);
+ * mean, for either dtype, two fp16 planes hi, lo with hi + lo = the block's
+ * fp32 mean times 2^e to 22-23 bits (e per block, max_d |mean_d| 2^e in
+ * [2^14, 2^15)), then 2^-e per block as fp32.  The mean of block blk of
+ * (b, g) is (hi + lo) * scale[(b * Hk + g) * NB + blk]. */
 int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sk_d,
                         int B, int Hk, int N, int D, int dtype, int mode, void* planes,
                         void* stream);
@@ -74,8 +79,8 @@ int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
  * Replaces src/sparse_attention.py:623-707 of _block_select_kv_idx_v2
  * (per-row scores :638-648, tile max :655-656, causal tile mask :660-666,
  * FMAX forcing :675-681, topk :697, margin :703-707).
- * q [B, H, M, D] in dtype, the planes' format (query head h uses KV head
- * h / (H / Hk));
+ * q [B, H, M, D] in dtype, planes from ugbsa_block_summary of the same
+ * dtype and mode (query head h uses KV head h / (H / Hk));
  * kv_idx out [B, H, Qt, k_slots] int32 contiguous, slots ordered by
  * (score desc, block asc); sigma out [B, H, Qt] fp32; tile_score (optional
  * diagnostic) out [B, H, Qt, NB] fp32 = the exact scores ranked.

@@ -107,34 +107,82 @@ def unexplained_differences(kv_a, kv_b, T_ref, k_base, k_slots, trig_a=None, tri
     return n_diff, bad
 
 
-def summation_bound(q, k, scaling, quest, fp16_planes=True):
+def summation_bound(q, k, scaling, quest):
     """Per (b, h, tile, block): how far two fp32 evaluations of a tile score
     may differ when they add the same exact products in different orders —
-    2 n 2^-24 (n = P D terms) times the row's sum of |terms|, maxed over the
-    tile's rows — plus, for fp16 mean planes, their lo-term step (2^-25 per
-    element; bf16 planes hold the fp32 mean exactly) and 1e-5.  fp16 x fp16
-    products carry 22 significant bits, bf16 x bf16 16, so with fp16 nearly
-    every fp32 addition rounds; with bf16 large scores do too."""
+    2 n 2^-24 (n = 2 D terms: two planes) times the row's sum of |terms|,
+    maxed over the tile's rows — plus, for the mean planes, what the two fp16
+    terms leave of the fp32 mean (2^-23 |m_d| + 2^-39 max_d |m_d| per element,
+    see ``mean_plane_bound``) and 1e-5.  fp16 x fp16 products carry 22
+    significant bits, bf16 x bf16 16, so with fp16 nearly every fp32 addition
+    rounds; with bf16 large scores do too."""
     B, H, M, D = q.shape
     Hk, N = k.shape[1], k.shape[2]
     grp, nb, qt = H // Hk, (N + 63) // 64, (M + 63) // 64
+    n = 2 * D
     if quest:
         kmin, kmax = OS.block_summaries(k, True)
-        planes, n = (np.abs(kmax), np.abs(kmin)), 2 * D
+        planes = (np.abs(kmax), np.abs(kmin))
     else:
-        planes, n = (np.abs(OS.block_summaries(k, False)),), 3 * D
+        planes = (np.abs(OS.block_summaries(k, False)),)
     bound = np.zeros((B, H, qt, nb), np.float64)
     for b in range(B):
         for h in range(H):
             qa = q[b, h].astype(np.float64)
             if quest:
                 a = np.maximum(qa, 0) @ planes[0][b, h // grp].T - np.minimum(qa, 0) @ planes[1][b, h // grp].T
+                rep = 0.0
             else:
                 a = np.abs(qa) @ planes[0][b, h // grp].T
-            a = np.concatenate([a, np.zeros((qt * 64 - M, nb))]).reshape(qt, 64, nb).max(axis=1)
-            lo = 0.0 if quest or not fp16_planes else D * 2.0 ** -25 * np.abs(qa).max()
-            bound[b, h] = (2 * n * 2.0 ** -24 * a + lo) * abs(scaling) + 1e-5
+                mx = planes[0][b, h // grp].max(axis=-1)                      # [nb]
+                rep = 2.0 ** -23 * a + 2.0 ** -39 * np.abs(qa).sum(axis=-1)[:, None] * mx[None]
+            r = 2 * n * 2.0 ** -24 * a + rep                                    # per row
+            r = np.concatenate([r, np.zeros((qt * 64 - M, nb))]).reshape(qt, 64, nb).max(axis=1)
+            bound[b, h] = r * abs(scaling) + 1e-5
     return bound
+
+
+def decode_mean_planes(planes, B, Hk, nb, D):
+    """A mean summary buffer of kernel 1 (flat, any 16-bit dtype) as float64
+    numpy (hi, lo, scale): hi / lo [B, Hk, NB, D] fp16 values, scale [B, Hk,
+    NB] the blocks' 2^-e."""
+    flat = planes.reshape(-1)
+    n = B * Hk * nb * 2 * D
+    hl = flat[:n].view(torch.float16).view(B, Hk, nb, 2, D).double().cpu().numpy()
+    sc = flat[n:n + 2 * B * Hk * nb].view(torch.float32).view(B, Hk, nb).double().cpu().numpy()
+    return hl[..., 0, :], hl[..., 1, :], sc
+
+
+def check_mean_planes(planes, k):
+    """Kernel 1's mean summary of k [B, Hk, N, D] (host tensor, 16-bit values)
+    against the exact block means (float64, F.pad zeros included):
+
+    * each block's scale 2^-e is a power of two with max_d |hi_d| in [2^14,
+      2^15] (hi_d = fp16 of m_d 2^e; all-zero blocks: hi = lo = 0, scale 1);
+    * (hi + lo) 2^-e within 2^-23 |m_d| + 2^-25 2^-e of the kernel's fp32 mean,
+      which sits within the fp32 summation bound 64 2^-24 mean_r |x| of the
+      exact mean;
+    * lo carries the bits hi drops: hi alone misses that bound somewhere.
+    Returns the reconstructed means."""
+    B, Hk, N, D = k.shape
+    nb = (N + 63) // 64
+    hi, lo, sc = decode_mean_planes(planes, B, Hk, nb, D)
+    kp = np.zeros((B, Hk, nb * 64, D))
+    kp[:, :, :N] = k.double().numpy()
+    blocks = kp.reshape(B, Hk, nb, 64, D)
+    exact = blocks.mean(axis=3)
+    mant, _ = np.frexp(sc)
+    assert (mant == 0.5).all(), "block scales are powers of two"
+    hmax = np.abs(hi).max(axis=-1)
+    zero = np.abs(exact).max(axis=-1) == 0
+    assert ((hmax >= 2.0 ** 14) & (hmax <= 2.0 ** 15) | zero).all()
+    assert (sc[zero] == 1.0).all() and (hi[zero] == 0).all() and (lo[zero] == 0).all()
+    rec = (hi + lo) * sc[..., None]
+    bound = (64 * 2.0 ** -24 * np.abs(blocks).mean(axis=3) + 2.0 ** -23 * np.abs(exact)
+             + 2.0 ** -25 * sc[..., None] + 1e-300)
+    assert (np.abs(rec - exact) <= bound).all(), np.abs(rec - exact).max()
+    assert not (np.abs(hi * sc[..., None] - exact) <= bound).all(), "lo term unused"
+    return rec
 
 
 # Attention bar of the contract (bf16 inputs, fp32 accumulation).

@@ -37,9 +37,10 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_size_queries(lib):
-    # [B, Hk, NB, P, D]: c3 Quest = 1 * 4 * 2048 * 2 * 128
+    # Quest [B, Hk, NB, 2, D]: c3 = 1 * 4 * 2048 * 2 * 128; mean: the two fp16
+    # planes, then one fp32 scale (two 16-bit elements) per block
     assert lib.ugbsa_summary_elems(1, 4, 131072, 128, _capi.MODE_QUEST) == 4 * 2048 * 2 * 128
-    assert lib.ugbsa_summary_elems(1, 2, 1000, 64, _capi.MODE_MEAN) == 2 * 16 * 3 * 64
+    assert lib.ugbsa_summary_elems(1, 2, 1000, 64, _capi.MODE_MEAN) == 2 * 16 * (2 * 64 + 2)
     # K and V operand copies, then the tile schedule (2 * B * NB int32 = 4 * B * NB bf16,
     # rounded to 16 bytes)
     assert lib.ugbsa_attn_workspace_elems(1, 4, 1000, 128) == 2 * 4 * 16 * 64 * 128 + 64

@@ -1,6 +1,6 @@
 """Generated-code checks of the selection kernel (CPU; needs hipcc).
 
-The launched select_kernel instances run at about 230-244 VGPRs and the
+The launched select_kernel instances run at about 180-234 VGPRs and the
 compiler parks some scalar values (kernel arguments, addresses) in VGPR lanes
 (`v_writelane_b32` / `v_readlane_b32`, SGPR spills) rather than in scratch.
 These tests compile select.hip with the library's flags and check, for the
@@ -26,12 +26,12 @@ sys.path.insert(0, ROOT)
 
 import __graft_entry__ as G  # noqa: E402
 
-# select_kernel<ElemBf16, D, P, KP, STREAM=false, ROWS=false>: c2 / c4 Quest
-# (128, 2, 128), c3 Quest (128, 2, 256), c4 K-mean (128, 3, 128 / 256), c5
-# K-mean at head_dim 256 (256, 3, 256)
+# select_kernel<ElemBf16, D, QUEST, KP, STREAM=false, ROWS=false>: c2 / c4
+# Quest (128, true, 128), c3 Quest (128, true, 256), c4 K-mean (128, false,
+# 128 / 256), c5 K-mean at head_dim 256 (256, false, 256)
 PREFIX = "_ZN5ugbsa13select_kernelINS_8ElemBf16E"
-INSTANCES = ["Li128ELi2ELi128ELb0ELb0", "Li128ELi2ELi256ELb0ELb0", "Li128ELi3ELi128ELb0ELb0",
-             "Li128ELi3ELi256ELb0ELb0", "Li256ELi3ELi256ELb0ELb0"]
+INSTANCES = ["Li128ELb1ELi128ELb0ELb0", "Li128ELb1ELi256ELb0ELb0", "Li128ELb0ELi128ELb0ELb0",
+             "Li128ELb0ELi256ELb0ELb0", "Li256ELb0ELi256ELb0ELb0"]
 LABEL = re.compile(r"^(\.LBB\d+_\d+:|; %bb\.\d+:)")
 
 

@@ -62,7 +62,7 @@ SIGNATURES = {
                             _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f,
                             _p, _i64, _i64, _i64, _i64, _p, _i64, _p]),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _LIB = None
 

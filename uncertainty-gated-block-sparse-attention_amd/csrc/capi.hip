@@ -72,7 +72,9 @@ const char* ugbsa_last_error(void) { return g_error.c_str(); }
 
 int64_t ugbsa_summary_elems(int B, int Hk, int N, int D, int mode) {
   const int64_t nb = (N + ugbsa::kBlock - 1) / ugbsa::kBlock;
-  return static_cast<int64_t>(B) * Hk * nb * (mode == UGBSA_MODE_QUEST ? 2 : 3) * D;
+  // Quest: two planes in the call's format; mean: two fp16 planes, then one
+  // fp32 scale (two 16-bit elements) per block
+  return static_cast<int64_t>(B) * Hk * nb * (mode == UGBSA_MODE_QUEST ? 2 * D : 2 * D + 2);
 }
 
 int64_t ugbsa_attn_workspace_elems(int B, int Hk, int N, int D) {

@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
 #include <utility>
 
 
@@ -338,6 +339,57 @@ __device__ __forceinline__ uint32_t wave_excl_scan(uint32_t x, int lane) {
     if (lane >= off) incl += y;
   }
   return incl - x;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x, int lane) {
+  x = max(x, xor_lanes<32>(x, lane));
+  x = max(x, xor_lanes<16>(x, lane));
+  x = max(x, xor_lanes<8>(x, lane));
+  x = max(x, xor_lanes<4>(x, lane));
+  x = max(x, xor_lanes<2>(x, lane));
+  return max(x, xor_lanes<1>(x, lane));
+}
+
+// The mean summary planes of kernel 1 ([B, Hk, NB, 2, D] fp16 hi / lo of
+// each block's fp32 mean scaled by 2^e) are followed by the blocks' 2^-e,
+// [B, Hk, NB] fp32.
+__host__ __device__ inline const float* mean_descale(const uint16_t* planes, int B, int Hk, int NB,
+                                                     int D) {
+  return reinterpret_cast<const float*>(planes + static_cast<int64_t>(B) * Hk * NB * 2 * D);
+}
+
+// NF fragments of a Q tile (format E) to fp16 in place, scaled by 2^qs with
+// qs chosen over the wavefront from the exponent field of the largest
+// magnitude so that max |q| 2^qs lies in [2^14, 2^15) (qs = 0 for an all-zero
+// tile).  Exact for every element within 2^29 of the largest: fp16 holds the
+// 8 (bf16) or 11 (fp16) significant bits, and its normal range spans 2^-14 ..
+// 2^15.  Returns 2^-qs, which undoes the scaling on a product exactly.
+template <typename E, int NF>
+__device__ __forceinline__ float q_tile_to_f16(bf16x8* f, int lane) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  u16x2 mv = {0, 0};
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const u32x4 w = __builtin_bit_cast(u32x4, f[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      mv = __builtin_elementwise_max(mv, __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu));
+  }
+  const uint32_t m = wave_max_u32(max(static_cast<uint32_t>(mv[0]), static_cast<uint32_t>(mv[1])), lane);
+  constexpr bool kF16 = E::code == 1;
+  const int qs = m == 0u ? 0 : (kF16 ? 29 - static_cast<int>(m >> 10) : 141 - static_cast<int>(m >> 7));
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    u32x4 w = __builtin_bit_cast(u32x4, f[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = ldexpf(E::to_f32(w[j] & 0xFFFFu), qs);
+      const float b = ldexpf(E::to_f32(w[j] >> 16), qs);
+      w[j] = ElemF16::pack2(a, b);
+    }
+    f[i] = __builtin_bit_cast(bf16x8, w);
+  }
+  return ldexpf(1.0f, -qs);
 }
 
 // Order LDS traffic of one wavefront against itself (no workgroup barrier).

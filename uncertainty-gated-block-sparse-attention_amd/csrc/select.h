@@ -4,8 +4,10 @@
 // materialising the per-row score tensor [B, H, M, NB]:
 //   per-row score   S[r, blk] = sum_p sum_d Qcat_p[r, d] * planes[blk, p, d] * scaling
 //                   (Quest: Qcat = (max(q,0), min(q,0)), planes = (Kmax, Kmin) —
-//                   the two-matmul form of :638-642; mean: Qcat = (q, q, q),
-//                   planes = hi/mid/lo of the fp32 block mean, :647-648);
+//                   the two-matmul form of :638-642; mean: Qcat = (q, q) in fp16
+//                   scaled by 2^qs per tile, planes = hi/lo of the block's fp32
+//                   mean scaled by 2^e, both scales undone exactly on the fp32
+//                   sum, :647-648);
 //   tile max        T[t, blk] = max over the 64 rows of tile t (:655-656; rows
 //                   past M are zero queries, as the reference's F.pad);
 //   visibility      blocks past the tile's last row are -inf (:660-666);
@@ -350,15 +352,19 @@ __host__ __device__ constexpr int select_chunk(int P, int D) { return P * D <= 2
 // W: pairs (waves) per workgroup; wpb: workgroups per (b, KV head); nbuf:
 // plane chunk buffers in LDS, 2 (double-buffered) or 1 (a second barrier
 // per chunk), as the launcher sized the workgroup's LDS.
-template <typename E, int D, int P, int KP, bool STREAM, bool ROWS>
+template <typename E, int D, bool QUEST, int KP, bool STREAM, bool ROWS>
 __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
-    const uint16_t* __restrict__ planes, int B, int Hk, int M, int N, int NB, int Qt, int grp,
+    const uint16_t* __restrict__ planes, const float* __restrict__ bscale, int B, int Hk, int M,
+    int N, int NB, int Qt, int grp,
     int W, int wpb, float scaling, int k_base, int k_slots, int want_sigma,
     int32_t* __restrict__ kv_idx, float* __restrict__ sigma, float* __restrict__ tile_score,
     const SelectAux aux, int nbuf) {
   constexpr int KS = D / 32;
   constexpr int R = KP / 64;
+  constexpr int P = 2;                              // planes per block
+  // MFMA format: Quest multiplies the input values; the mean planes are fp16
+  using EM = std::conditional_t<QUEST, E, ElemF16>;
   constexpr int CH = select_chunk(P, D);
   constexpr int NT = CH / 16;                       // MFMA column tiles per chunk
   constexpr int PIECES = CH * P * D / 8;            // 16-byte pieces per chunk
@@ -369,8 +375,8 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   // K-min plane.  The two signed copies of the Q tile are kept when they fit
   // (2 * 4 * KS fragments); at head_dim 256, and in the streaming rows that
   // hold extra state, only q is kept and the halves are formed per chunk.
-  constexpr bool SPLIT_LATE = P == 2 && (D > 128 || STREAM);
-  constexpr int QSETS = P == 2 && !SPLIT_LATE ? 2 : 1;
+  constexpr bool SPLIT_LATE = QUEST && (D > 128 || STREAM);
+  constexpr int QSETS = QUEST && !SPLIT_LATE ? 2 : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   const SelectLds L = select_lds(P, D, NB, KP, CH, STREAM);
 
@@ -432,7 +438,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       for (int ks = 0; ks < KS; ++ks) {
         const bf16x8 x = (active && row < M) ? load_bf16x8(qb + row * sq_m + 32 * ks + 8 * g4)
                                              : zero_bf16x8();
-        if constexpr (P == 2 && !SPLIT_LATE) {
+        if constexpr (QUEST && !SPLIT_LATE) {
           qf[0][mt][ks] = bf16_pos(x);
           qf[1][mt][ks] = bf16_neg(x);
         } else {
@@ -441,8 +447,24 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
       }
     }
   }
+  // mean: Q in fp16, scaled by 2^qs with max |q| 2^qs in [2^14, 2^15) over
+  // the tile (exact for every element within 2^29 of the tile's largest);
+  // tdesc = 2^-qs undoes it on the scores
+  float tdesc = 1.f;
+  if constexpr (!QUEST) tdesc = q_tile_to_f16<E, 4 * KS>(&qf[0][0][0], lane);
 
   const uint16_t* pl = planes + (static_cast<int64_t>(b) * Hk + g) * NB * P * D;
+  // mean: 2^-e of each block of the KV head; the chunk's are loaded into
+  // bsn one chunk ahead, with its planes
+  const float* bs = QUEST ? nullptr : bscale + (static_cast<int64_t>(b) * Hk + g) * NB;
+  float bsc[NT], bsn[NT];
+  auto scale_load = [&](int c, float (&dst)[NT]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int blk = c * CH + 16 * nt + r16;
+      dst[nt] = blk < NB ? bs[blk] : 0.f;
+    }
+  };
   constexpr int pieces_per_blk = P * D / 8;
   // chunks up to the workgroup's largest tile (a wave of the next tile
   // scores one block past its row, which its selection never reads)
@@ -491,11 +513,15 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   asm volatile("" : "+v"(pinf));
 
   fetch(0);
+  if constexpr (!QUEST) scale_load(0, bsc);
   store(0, 0);
   __syncthreads();
   for (int c = 0; c < n_chunks; ++c) {
     const bool more = c + 1 < n_chunks;
     if (more) fetch(c + 1);
+    if constexpr (!QUEST) {
+      if (more) scale_load(c + 1, bsn);
+    }
     if (active) {
       const uint16_t* chunk = chunk_buf(nbuf == 2 ? (c & 1) : 0);
       f32x4 acc[4][NT];
@@ -532,15 +558,20 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
             asm volatile("" : "+v"(x));
             a = p == 0 ? bf16_pos(x) : bf16_neg(x);
           } else {
-            a = qf[P == 2 ? p : 0][mt][ks];
+            a = qf[QSETS == 2 ? p : 0][mt][ks];
           }
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = E::mfma(a, bq[s % 3][nt], acc[mt][nt]);
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = EM::mfma(a, bq[s % 3][nt], acc[mt][nt]);
         }
         // keep each step's reads ahead of the previous step's MFMAs (the
         // scheduler would otherwise pair two steps' reads and wait on them)
         __builtin_amdgcn_sched_barrier(0);
       });
+      // the exact factor from the MFMA sums to the scores of column nt (1
+      // for Quest; a product of two powers of two for the mean)
+      float cs[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) cs[nt] = QUEST ? 1.f : bsc[nt] * tdesc;
       if constexpr (ROWS) {
         // per-row scores (the v1 selector's input): fl(raw * scaling), -inf
         // past the tile's visible blocks, rows past M skipped
@@ -556,7 +587,9 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
               const int r = 16 * mt + 4 * g4 + i;
               const int blk = c * CH + 16 * nt + r16;
               if (t * kBlock + r < M && blk < NB)
-                rs[static_cast<int64_t>(r) * NB + blk] = blk < n_vis ? acc[mt][nt][i] * scaling : -INFINITY;
+                rs[static_cast<int64_t>(r) * NB + blk] =
+                    blk < n_vis ? (QUEST ? acc[mt][nt][i] : acc[mt][nt][i] * cs[nt]) * scaling
+                                : -INFINITY;
             }
       } else {
         // tile max over the 64 rows of (score * scaling): the max (min for a
@@ -574,6 +607,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
             for (int i = 0; i < 4; ++i) mx = __builtin_amdgcn_fmed3f(mx, acc[mt][nt][i], bound);
           mx = quad_rows_med3(mx, bound);
           const int blk = c * CH + 16 * nt + r16;
+          if constexpr (!QUEST) mx *= cs[nt];
           if (g4 == nt % 4 && blk < NB) trow[STREAM ? 16 * nt + r16 : blk] = mx * scaling;
         }
         if constexpr (STREAM) {
@@ -606,6 +640,10 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
     }
     if (nbuf == 1) __syncthreads();       // every wave is done with the one buffer
     if (more) store(nbuf == 2 ? ((c + 1) & 1) : 0, c + 1);
+    if constexpr (!QUEST) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) bsc[nt] = bsn[nt];
+    }
     __syncthreads();
   }
   if (!active) return;   // no workgroup barrier follows
@@ -691,7 +729,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void select_kernel(
   }
 }
 
-template <typename E, int D, int P, int KP, bool STREAM, bool ROWS = false>
+template <typename E, int D, bool QUEST, int KP, bool STREAM, bool ROWS = false>
 static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                   const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                   float scaling, int k_base, int k_slots, int want_sigma,
@@ -700,7 +738,7 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   const int NB = (N + kBlock - 1) / kBlock;
   const int Qt = (M + kBlock - 1) / kBlock;
   const int grp = H / Hk;
-  const SelectLds L = select_lds(P, D, NB, KP, select_chunk(P, D), STREAM);
+  const SelectLds L = select_lds(2, D, NB, KP, select_chunk(2, D), STREAM);
   constexpr int kLdsMax = 160 * 1024;
   // W (tile, head) pairs per workgroup, one wavefront each: the W that
   // keeps the most wavefronts on a CU, given its LDS and at most 8 resident
@@ -729,18 +767,19 @@ static hipError_t launch_select_t(const uint16_t* q, int64_t sq_b, int64_t sq_h,
   const int tiles = ROWS ? aux.rows_t1 - aux.rows_t0 : Qt;
   const int wpb = (tiles * grp + W - 1) / W;        // workgroups per (b, KV head)
   const int64_t wgs = static_cast<int64_t>(B) * Hk * wpb;
-  auto kern = select_kernel<E, D, P, KP, STREAM, ROWS>;
+  auto kern = select_kernel<E, D, QUEST, KP, STREAM, ROWS>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds));
   if (e != hipSuccess) return e;
   kern<<<dim3(static_cast<unsigned>(wgs)), 64 * W, lds, stream>>>(
-      q, sq_b, sq_h, sq_m, planes, B, Hk, M, N, NB, Qt, grp, W, wpb, scaling, k_base,
+      q, sq_b, sq_h, sq_m, planes, QUEST ? nullptr : mean_descale(planes, B, Hk, NB, D), B, Hk,
+      M, N, NB, Qt, grp, W, wpb, scaling, k_base,
       k_slots, want_sigma, kv_idx, sigma, tile_score, aux, nbuf);
   return hipGetLastError();
 }
 
-template <typename E, int D, int P>
+template <typename E, int D, bool QUEST>
 static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_m,
                                    const uint16_t* planes, int B, int H, int Hk, int M, int N,
                                    float scaling, int k_base, int k_slots, int want_sigma,
@@ -748,7 +787,7 @@ static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h
                                    const SelectAux& aux, hipStream_t stream) {
   // per-row scores only: the smallest LDS layout (no row, no top-k)
   if (aux.row_scores != nullptr)
-    return launch_select_t<E, D, P, 64, true, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,
+    return launch_select_t<E, D, QUEST, 64, true, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,
                                                  scaling, 1, 1, 0, nullptr, nullptr, nullptr, aux,
                                                  stream);
   // rows of more than kStreamBlocks blocks stream their candidates, so that
@@ -756,10 +795,10 @@ static hipError_t launch_select_kp(const uint16_t* q, int64_t sq_b, int64_t sq_h
   const bool stream_rows = (N + kBlock - 1) / kBlock > kStreamBlocks;
 #define UGBSA_SEL(KP_)                                                                      \
   return stream_rows                                                                        \
-             ? launch_select_t<E, D, P, KP_, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, \
+             ? launch_select_t<E, D, QUEST, KP_, true>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, \
                                                 scaling, k_base, k_slots, want_sigma, kv_idx,  \
                                                 sigma, tile_score, aux, stream)                 \
-             : launch_select_t<E, D, P, KP_, false>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,  \
+             : launch_select_t<E, D, QUEST, KP_, false>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N,  \
                                                  scaling, k_base, k_slots, want_sigma, kv_idx, \
                                                  sigma, tile_score, aux, stream)
   if (k_slots <= 64) UGBSA_SEL(64);
@@ -779,14 +818,14 @@ hipError_t launch_select_e(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_
                          hipStream_t stream, const SelectAux* aux) {
   const SelectAux off{};
   const SelectAux& dm = aux != nullptr ? *aux : off;
-#define UGBSA_SELD(D_, P_)                                                                 \
-  return launch_select_kp<E, D_, P_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,    \
+#define UGBSA_SELD(D_, Q_)                                                                 \
+  return launch_select_kp<E, D_, Q_>(q, sq_b, sq_h, sq_m, planes, B, H, Hk, M, N, scaling,    \
                                   k_base, k_slots, want_sigma, kv_idx, sigma, tile_score,  \
                                   dm, stream)
   const bool quest = mode == kModeQuest;
-  if (D == 64) { if (quest) UGBSA_SELD(64, 2); else UGBSA_SELD(64, 3); }
-  if (D == 128) { if (quest) UGBSA_SELD(128, 2); else UGBSA_SELD(128, 3); }
-  if (D == 256) { if (quest) UGBSA_SELD(256, 2); else UGBSA_SELD(256, 3); }
+  if (D == 64) { if (quest) UGBSA_SELD(64, true); else UGBSA_SELD(64, false); }
+  if (D == 128) { if (quest) UGBSA_SELD(128, true); else UGBSA_SELD(128, false); }
+  if (D == 256) { if (quest) UGBSA_SELD(256, true); else UGBSA_SELD(256, false); }
 #undef UGBSA_SELD
   return hipErrorInvalidValue;
 }

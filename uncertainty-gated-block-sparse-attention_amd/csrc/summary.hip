@@ -5,14 +5,21 @@
 // copy; the summaries of repeated heads are identical).  Rows past N count as
 // zeros, as F.pad does for the last partial block.
 //
-// Output "planes" [B, Hk, NB, P, D] in K's 16-bit format (bf16 or fp16) is
-// the operand layout of the scoring kernel: P = 2 for Quest (K-max, K-min —
-// input values, exact) and P = 3 for the mean, stored as an unevaluated sum
-// hi + mid + lo of three 16-bit values, so the MFMA contraction
-// q . (hi + mid + lo) follows an fp32 q . mean: in bf16 to within an fp32
-// rounding of the mean; in fp16 the lo term can fall in fp16's subnormal
-// range, which bounds the error of the sum by 2^-25 absolute (against
-// 2^-24 relative for an fp32 mean).
+// Output "planes", the operand layout of the scoring kernel:
+//  * Quest: [B, Hk, NB, 2, D] in K's 16-bit format (bf16 or fp16): K-max,
+//    K-min — input values, exact.
+//  * mean, for both formats: [B, Hk, NB, 2, D] fp16, then [B, Hk, NB] fp32.
+//    The fp32 mean m of a block is scaled by 2^e, e = 141 - (the fp32
+//    exponent field of max_d |m_d|), so that max_d |m_d| 2^e lies in
+//    [2^14, 2^15), and stored as the unevaluated sum hi + lo of two fp16
+//    values (hi = fp16(m 2^e), lo = fp16(m 2^e - hi)); the fp32 array holds
+//    2^-e.  hi + lo carries 22-23 significant bits of each m_d 2^e: the sum
+//    is within 2^-23 |m_d| 2^e + 2^-25 of it (the second term where lo falls
+//    in fp16's subnormal range, i.e. 2^-39 of the block's largest |m_d|).
+//    The scoring kernel multiplies fp16 Q (scaled by a power of two per
+//    tile, exact) by both planes on the fp16 MFMA — two contractions per
+//    block instead of the three that a bf16 hi + mid + lo split of the fp32
+//    mean takes — and undoes both scales exactly on the fp32 result.
 #include "common.h"
 #include "launch.h"
 
@@ -21,7 +28,7 @@ namespace ugbsa {
 template <int D, typename E>
 __global__ __launch_bounds__(256) void block_summary_kernel(
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
-    int Hk, int N, int NB, int mode, uint16_t* __restrict__ planes) {
+    int B, int Hk, int N, int NB, int mode, uint16_t* __restrict__ planes) {
   constexpr int CH = D / 8;        // 16-byte chunks per row
   constexpr int RG = 256 / CH;     // row groups
   constexpr int RPG = kBlock / RG; // rows per group
@@ -57,26 +64,44 @@ __global__ __launch_bounds__(256) void block_summary_kernel(
   }
   __syncthreads();
 
-  const int P = mode == kModeQuest ? 2 : 3;
-  uint16_t* out = planes + ((static_cast<int64_t>(b) * Hk + h) * NB + blk) * P * D;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    if (mode == kModeQuest) {
+  if (mode == kModeQuest) {
+    uint16_t* out = planes + ((static_cast<int64_t>(b) * Hk + h) * NB + blk) * 2 * D;
+    for (int d = threadIdx.x; d < D; d += 256) {
       float a = -INFINITY, z = INFINITY;
       for (int g = 0; g < RG; ++g) { a = fmaxf(a, red[2][g][d]); z = fminf(z, red[1][g][d]); }
       out[d] = E::from_f32(a);          // exact: an input value (or 0)
       out[D + d] = E::from_f32(z);
-    } else {
-      float acc = 0.f;
-      for (int g = 0; g < RG; ++g) acc += red[0][g][d];
-      const float mean = acc * (1.0f / kBlock);
-      const uint16_t h0 = E::from_f32(mean);
-      const float r1 = mean - E::to_f32(h0);
-      const uint16_t h1 = E::from_f32(r1);
-      const float r2 = r1 - E::to_f32(h1);
-      out[d] = h0;
-      out[D + d] = h1;
-      out[2 * D + d] = E::from_f32(r2);
     }
+    return;
+  }
+  // mean: one d per thread (D <= 256 threads), the block's largest |mean|
+  // over d through LDS, then the scaled two-term fp16 split
+  __shared__ uint32_t wmax[4];
+  const int d = threadIdx.x;
+  float mean = 0.f;
+  if (d < D) {
+    float acc = 0.f;
+    for (int g = 0; g < RG; ++g) acc += red[0][g][d];
+    mean = acc * (1.0f / kBlock);
+  }
+  uint32_t mb = __float_as_uint(mean) & 0x7FFFFFFFu;     // |mean| orders as its bits
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mb = max(mb, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mb), m, 64)));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mb;
+  __syncthreads();
+  const uint32_t bmax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  const int e = bmax == 0u ? 0 : 141 - static_cast<int>(bmax >> 23);
+  const int64_t bid = (static_cast<int64_t>(b) * Hk + h) * NB + blk;
+  if (d < D) {
+    uint16_t* out = planes + bid * 2 * D;
+    const float x = ldexpf(mean, e);                   // exact
+    const uint16_t hi = ElemF16::from_f32(x);
+    out[d] = hi;
+    out[D + d] = ElemF16::from_f32(x - ElemF16::to_f32(hi));
+  }
+  if (threadIdx.x == 0) {
+    float* descale = reinterpret_cast<float*>(planes + static_cast<int64_t>(B) * Hk * NB * 2 * D);
+    descale[bid] = ldexpf(1.0f, -e);
   }
 }
 
@@ -88,13 +113,13 @@ static hipError_t launch_block_summary_e(const uint16_t* k, int64_t sk_b, int64_
   dim3 grid(NB, Hk, B);
   switch (D) {
     case 64:
-      block_summary_kernel<64, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
+      block_summary_kernel<64, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, B, Hk, N, NB, mode, planes);
       break;
     case 128:
-      block_summary_kernel<128, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
+      block_summary_kernel<128, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, B, Hk, N, NB, mode, planes);
       break;
     case 256:
-      block_summary_kernel<256, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, Hk, N, NB, mode, planes);
+      block_summary_kernel<256, E><<<grid, 256, 0, stream>>>(k, sk_b, sk_h, sk_n, B, Hk, N, NB, mode, planes);
       break;
     default:
       return hipErrorInvalidValue;

@@ -219,8 +219,10 @@ def select_v2(query, key_states, scaling, block_m=64, sel: Selector = None,
 
 
 def block_summary(key_states, mode):
-    """Kernel 1: the K-block summary planes [B, Hk, NB, P, D] (in K's dtype) of ``mode``
-    (``_capi.MODE_QUEST`` or ``_capi.MODE_MEAN``), on the current stream."""
+    """Kernel 1: the K-block summaries of ``mode`` (``_capi.MODE_QUEST`` or
+    ``_capi.MODE_MEAN``) as one flat buffer in K's dtype, on the current stream:
+    Quest [B, Hk, NB, 2, D] (K-max, K-min); mean the fp16 planes [B, Hk, NB, 2, D]
+    then the fp32 block scales [B, Hk, NB] (``block_means`` decodes them)."""
     B, Hk, N, D = key_states.shape
     lib = _capi.lib()
     key_states = _contig_rows(key_states)
@@ -231,6 +233,15 @@ def block_summary(key_states, mode):
                                         _capi.stream_ptr(key_states.device)),
                 "block summary")
     return planes
+
+
+def block_means(planes, B, Hk, nb, D):
+    """The fp32 block means [B, Hk, NB, D] held by a mean summary buffer of
+    ``block_summary``: (hi + lo) * 2^-e per block (hi, lo fp16)."""
+    n = B * Hk * nb * 2 * D
+    hl = planes[:n].view(torch.float16).view(B, Hk, nb, 2, D).float()
+    scale = planes[n:n + 2 * B * Hk * nb].view(torch.float32).view(B, Hk, nb, 1)
+    return (hl[..., 0, :] + hl[..., 1, :]) * scale
 
 
 def use_quest(sel: Selector = None) -> bool:
@@ -310,7 +321,7 @@ def select_mask_v1(query, key_states, scaling, sel: Selector = None, want_scores
     planes = block_summary(key_states, mode)
     if mode == _capi.MODE_MEAN and M > 1 and layer_idx is not None:
         # the mean K of each block, repeat_kv'd, cached for later planners (:230-232)
-        kp = planes.view(B, Hk, nb, 3, D).float().sum(3).repeat_interleave(H // Hk, dim=1)
+        kp = block_means(planes, B, Hk, nb, D).repeat_interleave(H // Hk, dim=1)
         sel.k_pool_at[layer_idx] = kp.to(query.dtype)
     k_bud = min(int(max(min(sel.k_max, sel.budget_blocks), sel.k_min)), nb)
     router = sel.mode == "router"
