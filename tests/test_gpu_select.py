@@ -150,6 +150,39 @@ def test_select_pair_blocks_batch_and_ragged_groups(hip_lib, D, policy):
     assert (np.abs(T_or[fin] - T_k[fin]) <= tol[fin]).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("policy", ["topk", "router_mean_row_q"])
+def test_select_mean_planes_wide_magnitudes(hip_lib, dtype, D, policy):
+    """K-mean scoring with Q tiles and K blocks whose magnitudes span many
+    octaves (bf16: 2^-20 .. 2^20 per tile / block, rows within a tile over
+    2^-8 .. 1; fp16: 2^-6 .. 2^6), so that the per-block plane scales and the
+    per-tile Q scales move far from 1 and differ between neighbours: kv_idx /
+    sigma bit-exact on the kernel's own scores, and the scores within the
+    fp32 summation-order bound of the oracle's (relative to the terms' size)."""
+    print(f"[case] select wide magnitudes dtype={dtype} D={D} policy={policy}", flush=True)
+    g = torch.Generator().manual_seed(D + (7 if dtype == torch.float16 else 0))
+    B, H, Hk, S = 1, 4, 2, 1500
+    span = 20 if dtype == torch.bfloat16 else 6
+    nb = (S + 63) // 64
+    tile_sc = torch.pow(2.0, torch.randint(-span, span + 1, (B, H, nb, 1), generator=g).float())
+    row_sc = torch.pow(2.0, torch.randint(-8, 1, (B, H, nb * 64, 1), generator=g).float())
+    blk_sc = torch.pow(2.0, torch.randint(-span, span + 1, (B, Hk, nb, 1), generator=g).float())
+    q = torch.randn(B, H, S, D, generator=g) * (tile_sc.repeat_interleave(64, 2) * row_sc)[:, :, :S]
+    k = torch.randn(B, Hk, S, D, generator=g) * blk_sc.repeat_interleave(64, 2)[:, :, :S]
+    q, k = q.to(dtype), k.to(dtype)
+    sel = make_sel(budget_blocks=3, k_min=1, **POLICIES[policy])
+    res, _ = gpu_vs_oracle_on_kernel_scores(q, k, D ** -0.5, sel)
+    T_or = OS.tile_scores(q.float().numpy(), k.float().numpy(), D ** -0.5, False)
+    T_k = res.tile_score.cpu().numpy()
+    fin = np.isfinite(T_or)
+    assert np.array_equal(fin, np.isfinite(T_k))
+    tol = summation_bound(q.float().numpy(), k.float().numpy(), D ** -0.5, False)
+    d = np.abs(T_or[fin].astype(np.float64) - T_k[fin])
+    assert (d <= tol[fin]).all(), (d.max(), (d / tol[fin]).max())
+    print(f"  max |dT| / bound = {(d / tol[fin]).max():.3f}", flush=True)
+
+
 @pytest.mark.parametrize("name", ["a", "b_ragged", "c_full"])
 def test_select_vs_reference_golden(hip_lib, name):
     """The reference's own kv_idx (fp32 CPU run) reproduced on the GPU."""
