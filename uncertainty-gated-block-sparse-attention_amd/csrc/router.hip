@@ -13,29 +13,35 @@
 // ((k_quant - 1) / H + 1)-th smallest per-tile mean.
 //
 // The threshold needs every tile's sigma, so it runs as one 1024-thread
-// workgroup (an 8-bit radix select, 4 passes over <= B * H * Qt values that
-// sit in L2), followed by a grid-wide fill.
+// workgroup (an 8-bit radix select, 4 passes), followed by a grid-wide fill.
+// With row grain the per-tile head means stay in LDS while B * Qt <=
+// kRouterLdsMeans (every BASELINE shape, 1M tokens included), so the radix
+// passes and the decisions read LDS rather than L2; larger inputs and cell
+// grain select over sigma_eff in global memory.
 #include "common.h"
 #include "launch.h"
 
 namespace ugbsa {
 
 // Sum over h = 0 .. H-1 of x[h * stride], added in head order (the order of
-// ATen's CPU sum that the reference's mean runs), with the loads issued eight
+// ATen's CPU sum that the reference's mean runs), with the loads issued NL
 // at a time so that their latencies overlap.
+template <int NL = 8>
 __device__ __forceinline__ float head_sum_in_order(const float* __restrict__ x, int H,
                                                    int64_t stride) {
   float acc = 0.f;
-  for (int h0 = 0; h0 < H; h0 += 8) {
-    float v[8];
+  for (int h0 = 0; h0 < H; h0 += NL) {
+    float v[NL];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = h0 + j < H ? x[(h0 + j) * stride] : 0.f;
+    for (int j = 0; j < NL; ++j) v[j] = h0 + j < H ? x[(h0 + j) * stride] : 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < NL; ++j)
       if (h0 + j < H) acc = h0 + j == 0 ? v[0] : acc + v[j];
   }
   return acc;
 }
+
+constexpr int kRouterLdsMeans = 16384;   // per-tile means held in LDS (64 KiB)
 
 // k-th smallest (1-based) of value_at(0 .. n - 1) by one workgroup: a
 // 4-pass 8-bit radix select over the order-preserving float keys (NaN above
@@ -98,17 +104,25 @@ __global__ __launch_bounds__(1024) void router_threshold_kernel(
     float* __restrict__ threshold) {
   __shared__ uint32_t hist[256 * kRouterWaves];
   __shared__ uint32_t s_prefix, s_remaining;
+  extern __shared__ float smean[];          // [B * Qt] when in_lds
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t n_all = static_cast<int64_t>(B) * H * Qt;
+  const int64_t n_tiles = static_cast<int64_t>(B) * Qt;
+  const bool in_lds = grain == kGrainRow && n_tiles <= kRouterLdsMeans;
 
-  // 1. effective sigma
+  // 1. effective sigma (with in_lds, sigma_eff is written with the decisions)
   if (grain == kGrainRow) {
-    for (int64_t i = tid; i < static_cast<int64_t>(B) * Qt; i += nt) {
-      const int b = static_cast<int>(i / Qt), t = static_cast<int>(i % Qt);
-      const float acc = head_sum_in_order(sigma + (static_cast<int64_t>(b) * H) * Qt + t, H, Qt);
-      const float mean = acc / static_cast<float>(H);
-      for (int h = 0; h < H; ++h) sigma_eff[(static_cast<int64_t>(b) * H + h) * Qt + t] = mean;
-    }
+    for (int b = 0; b < B; ++b)
+      for (int t = tid; t < Qt; t += nt) {
+        const float acc =
+            head_sum_in_order<32>(sigma + (static_cast<int64_t>(b) * H) * Qt + t, H, Qt);
+        const float mean = acc / static_cast<float>(H);
+        if (in_lds) {
+          smean[b * Qt + t] = mean;
+        } else {
+          for (int h = 0; h < H; ++h) sigma_eff[(static_cast<int64_t>(b) * H + h) * Qt + t] = mean;
+        }
+      }
   } else {
     for (int64_t i = tid; i < n_all; i += nt) sigma_eff[i] = sigma[i];
   }
@@ -118,9 +132,10 @@ __global__ __launch_bounds__(1024) void router_threshold_kernel(
   float thr = tau;
   if (rmode == kRouterQuantile) {
     // rank among the values examined: per-tile means (row) or all cells
-    const int64_t n = grain == kGrainRow ? static_cast<int64_t>(B) * Qt : n_all;
+    const int64_t n = grain == kGrainRow ? n_tiles : n_all;
     const int64_t kth = grain == kGrainRow ? (k_quant - 1) / H + 1 : k_quant;  // 1-based
     auto value_at = [&](int64_t i) -> float {
+      if (in_lds) return smean[i];
       if (grain == kGrainRow) {
         const int64_t b = i / Qt, t = i % Qt;
         return sigma_eff[(b * H) * Qt + t];
@@ -132,9 +147,21 @@ __global__ __launch_bounds__(1024) void router_threshold_kernel(
   if (tid == 0 && threshold != nullptr) *threshold = thr;
 
   // 3. decision (NaN never triggers: comparisons with NaN are false)
-  for (int64_t i = tid; i < n_all; i += nt) {
-    const float e = sigma_eff[i];
-    uncertain[i] = rmode == kRouterQuantile ? (e <= thr) : (e < tau);
+  if (in_lds) {
+    for (int bh = 0; bh < B * H; ++bh) {
+      const float* mrow = smean + (bh / H) * Qt;
+      const int64_t r0 = static_cast<int64_t>(bh) * Qt;
+      for (int t = tid; t < Qt; t += nt) {
+        const float e = mrow[t];
+        sigma_eff[r0 + t] = e;
+        uncertain[r0 + t] = rmode == kRouterQuantile ? (e <= thr) : (e < tau);
+      }
+    }
+  } else {
+    for (int64_t i = tid; i < n_all; i += nt) {
+      const float e = sigma_eff[i];
+      uncertain[i] = rmode == kRouterQuantile ? (e <= thr) : (e < tau);
+    }
   }
 }
 
@@ -154,9 +181,16 @@ hipError_t launch_router(const float* sigma, int B, int H, int Qt, int grain, in
                          float tau, int64_t k_quant, int32_t* kv_idx, int k_base, int k_slots,
                          int NB, float* sigma_eff, uint8_t* uncertain, float* threshold,
                          hipStream_t stream) {
-  router_threshold_kernel<<<1, 1024, 0, stream>>>(sigma, B, H, Qt, grain, rmode, tau, k_quant,
-                                                  sigma_eff, uncertain, threshold);
-  hipError_t e = hipGetLastError();
+  const int64_t n_tiles = static_cast<int64_t>(B) * Qt;
+  const size_t lds = grain == kGrainRow && n_tiles <= kRouterLdsMeans
+                         ? static_cast<size_t>(n_tiles) * sizeof(float) : 0;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_threshold_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     kRouterLdsMeans * static_cast<int>(sizeof(float)));
+  if (e != hipSuccess) return e;
+  router_threshold_kernel<<<1, 1024, lds, stream>>>(sigma, B, H, Qt, grain, rmode, tau, k_quant,
+                                                    sigma_eff, uncertain, threshold);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = static_cast<int64_t>(B) * H * Qt;
   const int64_t total = rows * (k_slots - k_base);
