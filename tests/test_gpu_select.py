@@ -346,13 +346,15 @@ def test_select_streaming_rows_exact(hip_lib, case):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("policy", ["topk", "router_mean_row_q"])
-def test_select_streaming_rows_mean_planes_d256(hip_lib, policy, dtype):
-    """Streaming rows at head_dim 256 with the three mean planes: a 24 KiB
-    plane chunk, which the launcher stages through one chunk buffer (a
-    second barrier per chunk) so that two workgroups share a CU.  kv_idx /
-    sigma bit-identical to the oracle on the kernel's own scores."""
-    print(f"[case] select streaming D=256 policy={policy} dtype={dtype}", flush=True)
-    nb = 4097
+@pytest.mark.parametrize("nb", [3000, 4097])
+def test_select_long_rows_mean_planes_d256(hip_lib, policy, dtype, nb):
+    """Long rows at head_dim 256 with the mean planes (16.6 KiB plane
+    chunks): 3000 blocks keep the row in LDS (12 KiB per wave) and the
+    launcher stages the chunks through one buffer (a second barrier per
+    chunk), so that two workgroups share a CU; 4097 blocks stream their
+    candidates.  kv_idx / sigma bit-identical to the oracle on the kernel's
+    own scores."""
+    print(f"[case] select long rows D=256 nb={nb} policy={policy} dtype={dtype}", flush=True)
     S = nb * 64
     g = torch.Generator().manual_seed(78)
     q = torch.randn(1, 2, S, 256, generator=g).to(dtype)

@@ -106,10 +106,11 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// Element formats of the 16-bit tensors (Q, K, V, the summary planes and the
-// attention output of one call share one).  Products of two 16-bit values
-// are exact in fp32 for both, so the fp32-accumulated scores and S = Q.K^T
-// follow the same arithmetic in either format.
+// Element formats of the 16-bit tensors (Q, K, V, the Quest summary planes
+// and the attention output of one call share one; the mean summary planes
+// are fp16 for both).  Products of two 16-bit values are exact in fp32 for
+// both, so the fp32-accumulated scores and S = Q.K^T follow the same
+// arithmetic in either format.
 struct ElemBf16 {
   static constexpr int code = 0;
   __device__ static __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
