@@ -188,18 +188,14 @@ __device__ __forceinline__ void select_to_cand(const float* trow, int n_vis, int
       const int common = diff ? __clz(static_cast<int>(diff)) : 32;
       pmask = common ? (0xFFFFFFFFu << (32 - common)) : 0u;
       prefix = kand & pmask;
-      // keys outside the common prefix (the forced ones, and any score that
-      // does not share it): above or below the whole prefix range
-      int above = 0, below = 0;
-      static_for<RK>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        if (j < jmax) {
-          const bool valid = lane + 64 * j < n_vis;
-          const uint32_t kp = key[j] & pmask;
-          above += __popcll(__ballot(valid && kp > prefix));
-          below += __popcll(__ballot(valid && kp < prefix));
-        }
-      });
+      // keys outside the common prefix, above or below its whole range: only
+      // positions 0 and n_vis - 1 (n_vis > K >= 1, so two of them), which the
+      // AND / OR leaves out — every other key shares the prefix by
+      // construction — so their two keys decide the counts
+      const uint32_t kf = float_key(trow[0]) & pmask;
+      const uint32_t kl = float_key(trow[n_vis - 1]) & pmask;
+      const int above = (kf > prefix ? 1 : 0) + (kl > prefix ? 1 : 0);
+      const int below = (kf < prefix ? 1 : 0) + (kl < prefix ? 1 : 0);
       remaining = K - above;
       fast = remaining > 0 && remaining <= n_vis - above - below;
       if (fast) {
