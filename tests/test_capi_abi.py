@@ -56,6 +56,9 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -3
     rc = lib.ugbsa_block_summary(16, 0, 0, 8, 1, 1, 1, 64, 96, _capi.DTYPE_BF16, _capi.MODE_MEAN, 16, None)
     assert rc == -1 and b"head_dim" in lib.ugbsa_last_error()
+    # the summary buffer (whose mean scales are fp32) must be 16-byte aligned
+    rc = lib.ugbsa_block_summary(16, 0, 0, 8, 1, 1, 1, 64, 128, _capi.DTYPE_BF16, _capi.MODE_MEAN, 18, None)
+    assert rc == -2 and b"planes" in lib.ugbsa_last_error()
     rc = lib.ugbsa_attn_fwd(16, 0, 0, 8, 2, 16, 0, 0, 8, 1, 16, 0, 0, 8, 1, 16, 0, 0, 0, 1,
                             1, 8, 2, 64, 64, 128, _capi.DTYPE_BF16, 1, 1, 64, 0.1,
                             16, 0, 0, 8, 1, 16, 1 << 40, None)

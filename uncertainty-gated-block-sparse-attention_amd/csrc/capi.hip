@@ -92,6 +92,9 @@ int ugbsa_block_summary(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_n,
   if (N < 1) return fail(UGBSA_EARG, "N must be positive");
   if (mode != UGBSA_MODE_MEAN && mode != UGBSA_MODE_QUEST) return fail(UGBSA_EARG, "unknown score mode %d", mode);
   if (planes == nullptr) return fail(UGBSA_EARG, "planes is null");
+  // the mean's fp32 block scales follow the planes; the selection reads
+  // the planes with 16-byte loads
+  if (!aligned16(planes)) return fail(UGBSA_ELAYOUT, "planes must be 16-byte aligned");
   return hip_result(ugbsa::launch_block_summary(static_cast<const uint16_t*>(k), sk_b, sk_h, sk_n, B, Hk, N, D,
                                                 dtype, mode, static_cast<uint16_t*>(planes),
                                                 static_cast<hipStream_t>(stream)),
