@@ -29,6 +29,57 @@ def test_header_and_binding_agree():
     assert declared_symbols() == sorted(_capi.SIGNATURES)
 
 
+def declared_prototypes():
+    """{name: (return C type, [parameter C types])} from the header's declarations."""
+    text = re.sub(r"/\*.*?\*/", " ", open(HEADER).read(), flags=re.S)
+    protos = {}
+    for ret, name, params in re.findall(
+            r"^\s*(const char\*|int64_t|int)\s+(ugbsa_\w+)\(([^)]*)\);", text, re.M):
+        params = " ".join(params.split())
+        types = []
+        if params not in ("", "void"):
+            for p in params.split(","):
+                # drop the parameter name: the type is everything before it
+                types.append(re.sub(r"\s*\b\w+$", "", p.strip()).replace(" *", "*"))
+        protos[name] = (ret, types)
+    return protos
+
+
+def _ctype_of(c_type):
+    if c_type.endswith("*"):
+        return ctypes.c_char_p if c_type == "const char*" else ctypes.c_void_p
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}[c_type]
+
+
+def test_binding_signatures_match_header_prototypes():
+    # every argument of every entry point has the ctypes class of its C type:
+    # an argument added, dropped or retyped on one side fails here on the CPU
+    protos = declared_prototypes()
+    assert sorted(protos) == declared_symbols()
+    for name, (ret, params) in protos.items():
+        res, args = _capi.SIGNATURES[name]
+        assert res is _ctype_of(ret), (name, ret, res)
+        assert len(args) == len(params), (name, len(args), len(params))
+        for i, (c_type, a) in enumerate(zip(params, args)):
+            want = ctypes.c_void_p if c_type.endswith("*") else _ctype_of(c_type)
+            assert a is want, (name, i, c_type, a)
+
+
+def test_prototype_parser_sees_a_planted_mismatch():
+    # the check above rests on the parser: a binding with one argument too few
+    # or one 32-bit integer where the header has int64_t must not pass
+    protos = declared_prototypes()
+    ret, params = protos["ugbsa_attn_workspace_elems"]
+    assert ret == "int64_t" and params == ["int"] * 4
+    ret, params = protos["ugbsa_router"]
+    assert params[7] == "int64_t" and params[0].endswith("*")
+    res, args = _capi.SIGNATURES["ugbsa_router"]
+    bad = list(args)
+    bad[7] = ctypes.c_int
+    assert bad[7] is not (ctypes.c_void_p if params[7].endswith("*") else _ctype_of(params[7]))
+    assert len(args[:-1]) != len(params)
+
+
 def test_library_exports_every_declared_symbol(lib):
     raw = ctypes.CDLL(_capi.LIB_PATH)
     for name in declared_symbols():
