@@ -20,7 +20,8 @@ namespace ugbsa {
 // values exceeds 2^kLazyLog2 (commit) are the row maxima formed, l and O
 // rescaled and P recomputed — after the first blocks a rare event.  K and
 // V^T operands are prefetched into registers two half blocks ahead (K(u+3)
-// is requested after phase 1, V^T(u+2) after phase 2); the two S, K and V
+// is requested during phase 2, one 1 KiB slab per two MFMA pairs, V^T(u+2)
+// after phase 2); the two S, K and V
 // register sets alternate between consecutive steps (the loop is unrolled by
 // 2).  Half blocks keep the live set at about 470 registers: O^T 128, two S
 // 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K 64, two V^T 64.
@@ -564,11 +565,13 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
   // Phase 2 without SB: the P.V MFMAs row set by row set; once
   // row set nt' of P(u) has been read, row set nt' of P(u+1) is computed
   // (elements 8 nt' .. 8 nt' + 7 of S(u+1), over the next DT / 2 pairs).
-  auto phase2s = [&](const SBuf& nx, const VSet& vf) {
+  // on_pair(j) issues this step's share of the next K loads before pair j.
+  auto phase2s = [&](const SBuf& nx, const VSet& vf, auto&& on_pair) {
     constexpr int PPN = DT / 2, EPN = 8 / PPN;
     static_assert(PPN * (NT / 2 + 1) <= P2, "row sets of P(u+1) fit in phase 2");
 #pragma unroll
     for (int j = 0; j < P2; ++j) {
+      on_pair(j);
 #pragma unroll
       for (int jj = 2 * j; jj < 2 * j + 2; ++jj) {
         const int nt = jj / DT, dt = jj % DT;
@@ -655,7 +658,7 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     const int rk = blk_raw(u + 3), rm1 = blk_raw(u + 1), rv = blk_raw(u + 2);
     phase1(cur, nxt, kc);
     commit(cur);
-    load_k(uni(rk), clamp_u(u + 3) & 1, kc);
+    gchar* kp = k_ptr(uni(rk), clamp_u(u + 3) & 1);
     // P and the row sums are only read later; pin them so that their
     // computation is not sunk past the mask branch into phase 2
 #pragma unroll
@@ -665,7 +668,14 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
       pb[nt] = __builtin_bit_cast(bf16x8, pin);
     }
     mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
-    phase2s(nxt, vc);
+    // K(u+3) into kc (free once phase 1 has read K(u+1)): one slab every
+    // second MFMA pair of phase 2 rather than all eight at once, so the four
+    // waves of a CU do not load in bursts (c2 / c3 / c4 attention 1.0-1.4 %
+    // faster than the burst after phase 1, same box)
+    static_assert(P2 >= 4 * KS, "every K slab is requested within phase 2");
+    phase2s(nxt, vc, [&](int j) {
+      if ((j & 1) == 0 && j / 2 < 2 * KS) kc[(j / 2) / KS][(j / 2) % KS] = slab(kp, j / 2);
+    });
     load_v(uni(rv), clamp_u(u + 2) & 1, vc);
   };
 
