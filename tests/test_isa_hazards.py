@@ -11,8 +11,9 @@ gfx950 assembly:
   basic block (a block may be entered right after any MFMA), so the VALU
   reads of the accumulators (rescale, epilogue) and any copy of them wait for
   the matrix core;
-* every inline-asm MFMA pair starts with `s_nop 1`, the two wait states a VALU
-  write of an MFMA operand needs;
+* no VALU instruction writes an A, B or C operand register of an inline-asm
+  MFMA fewer than two wait states before it on any path into it (the pairs
+  carry no s_nop of their own);
 * the kernel uses no scratch and no packed-fp32 VALU forms.
 """
 
@@ -163,15 +164,97 @@ def test_hazard_check_flags_an_early_read():
     assert agpr_hazards(loop[:-2] + drained[4:9] + loop[-2:])[0] == []
 
 
+VALU_TO_MFMA_WAIT_STATES = 2
+
+
+def _regs(operand):
+    """Register set {(file, index)} of one operand text (v7, a[4:7], ...)."""
+    m = re.match(r"([va])\[(\d+):(\d+)\]", operand)
+    if m:
+        return {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r"([va])(\d+)$", operand)
+    return {(m.group(1), int(m.group(2)))} if m else set()
+
+
+def _instrs(lines):
+    """(instruction, inside inline asm) of a block's lines, labels and
+    directives dropped."""
+    out, in_asm = [], False
+    for line in lines:
+        raw = line.strip()
+        if raw.startswith(";;#ASMSTART"):
+            in_asm = True
+        elif raw.startswith(";;#ASMEND"):
+            in_asm = False
+        else:
+            s = line.split(";")[0].strip()
+            if s and not s.startswith("."):
+                out.append((s, in_asm))
+    return out
+
+
+def operand_write_hazards(body):
+    """(writer, MFMA, wait states between them) for every VALU instruction
+    that writes an operand register of an inline-asm MFMA fewer than
+    VALU_TO_MFMA_WAIT_STATES wait states before it, on any path through the
+    kernel's control flow; plus the number of inline-asm MFMAs."""
+    blocks = _blocks(body)
+    ins = [_instrs(b[1]) for b in blocks]
+    index = {b[0]: i for i, b in enumerate(blocks) if b[0] is not None}
+    preds = [[] for _ in blocks]
+    for i, (_, _, succ, falls) in enumerate(blocks):
+        for lab in succ:
+            preds[index[lab]].append(i)
+        if falls and i + 1 < len(blocks):
+            preds[i + 1].append(i)
+    bad, mfmas = [], 0
+    for i in range(len(blocks)):
+        for k, (s, in_asm) in enumerate(ins[i]):
+            if not (in_asm and s.startswith("v_mfma")):
+                continue
+            mfmas += 1
+            ops = [o.strip() for o in s.split(None, 1)[1].split(",")]
+            srcs = set().union(*(_regs(o) for o in ops[1:4]))
+            stack, seen = [(i, k - 1, 0)], set()
+            while stack:
+                bi, j, ws = stack.pop()
+                while j >= 0 and ws < VALU_TO_MFMA_WAIT_STATES:
+                    p = ins[bi][j][0]
+                    op = p.split()[0]
+                    if op.startswith("v_") and len(p.split()) > 1:
+                        if _regs(p.split(None, 1)[1].split(",")[0].strip()) & srcs:
+                            bad.append((p, s, ws))
+                    ws += int(p.split()[1], 0) + 1 if op == "s_nop" else 1
+                    j -= 1
+                if j < 0 and ws < VALU_TO_MFMA_WAIT_STATES:
+                    for q in preds[bi]:
+                        if (q, ws) not in seen:
+                            seen.add((q, ws))
+                            stack.append((q, len(ins[q]) - 1, ws))
+    return bad, mfmas
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
-def test_asm_mfma_pairs_start_with_two_wait_states(asm, kernel):
-    body = "\n".join(kernel_body(asm, kernel))
-    blocks = re.findall(r";;#ASMSTART\n(.*?);;#ASMEND", body, re.S)
-    pairs = [b for b in blocks if "v_mfma" in b]
-    assert pairs
-    for b in pairs:
-        ins = [l.strip() for l in b.split("\n") if l.strip()]
-        assert ins[0] == "s_nop 1", ins
+def test_asm_mfma_operands_not_written_just_before(asm, kernel):
+    bad, mfmas = operand_write_hazards(kernel_body(asm, kernel))
+    assert not bad, bad[:5]
+    assert mfmas >= 64, mfmas
+
+
+def test_operand_hazard_check_flags_a_late_write():
+    # the checker itself, on hand-written snippets
+    mfma = [";;#ASMSTART", "v_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[4:7], a[0:3]", ";;#ASMEND"]
+    body = ["v_cvt_pk_bf16_f32 v5, v8, v9", "v_mov_b32_e32 v20, v21"] + mfma
+    assert operand_write_hazards(body) == ([("v_cvt_pk_bf16_f32 v5, v8, v9", mfma[1], 1)], 1)
+    assert operand_write_hazards(body[:1] + ["s_nop 1"] + body[1:])[0] == []
+    # an accumulator written by v_accvgpr_write at the end of a predecessor block
+    # (the branch back to the MFMA is the one wait state between them)
+    loop = [".LBB0_1:"] + mfma + ["s_cbranch_scc1 .LBB0_2", "v_accvgpr_write_b32 a2, v3",
+                                  "s_branch .LBB0_1", ".LBB0_2:", "s_endpgm"]
+    assert operand_write_hazards(loop)[0] == [("v_accvgpr_write_b32 a2, v3", mfma[1], 1)]
+    # writes of other registers, or of the operands two wait states earlier, pass
+    assert operand_write_hazards(["v_mov_b32_e32 v4, v9", "v_add_f32_e32 v30, v1, v2",
+                                  "v_mov_b32_e32 v31, v1"] + mfma)[0] == []
 
 
 @pytest.mark.parametrize("kernel", KERNELS)

@@ -144,23 +144,25 @@ struct ElemF16 {
 // accumulators never leave the AGPR file).  Written as inline assembly
 // because the compiler, built with MFMA results in VGPRs, would otherwise
 // place every accumulator there; its hazard recognizer does not look inside
-// the asm, so the wait states are explicit: s_nop 1 gives the two a VALU
-// write of an operand needs before an MFMA reads it (A, B, or the
-// accumulator after v_accvgpr_write), and agpr_drain() the ones a VALU read
-// of the results needs after the last MFMA.
+// the asm, so the wait states are the caller's: a VALU write of an operand
+// (A, B, or the accumulator after v_accvgpr_write) needs two before an MFMA
+// reads it, and agpr_drain() gives the ones a VALU read of the results needs
+// after the last MFMA.  The pair itself carries no s_nop: in the attention
+// loop its operands are V^T fragments from memory, P formed a phase earlier
+// and accumulators only these MFMAs write (a blanket s_nop 1 per pair cost
+// 0.6 % at head_dim 256); tests/test_isa_hazards.py checks the emitted code
+// for a VALU write of an operand within two wait states of the MFMA.
 template <typename E>
 __device__ __forceinline__ void mfma16x16x32_agpr2(f32x4& c0, bf16x8 a0, bf16x8 b0, f32x4& c1,
                                                    bf16x8 a1, bf16x8 b1) {
   if constexpr (E::code == ElemF16::code) {
     asm volatile(
-        "s_nop 1\n\t"
         "v_mfma_f32_16x16x32_f16 %0, %2, %3, %0\n\t"
         "v_mfma_f32_16x16x32_f16 %1, %4, %5, %1"
         : "+a"(c0), "+a"(c1)
         : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
   } else {
     asm volatile(
-        "s_nop 1\n\t"
         "v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\t"
         "v_mfma_f32_16x16x32_bf16 %1, %4, %5, %1"
         : "+a"(c0), "+a"(c1)
