@@ -21,18 +21,18 @@ namespace ugbsa {
 // rescaled and P recomputed — after the first blocks a rare event.  K and
 // V^T operands are prefetched into registers two half blocks ahead (K(u+3)
 // is requested during phase 2, one 1 KiB slab per two MFMA pairs, V^T(u+2)
-// after phase 2); the two S, K and V
-// register sets alternate between consecutive steps (the loop is unrolled by
-// 2).  Half blocks keep the live set at about 470 registers: O^T 128, two S
-// 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K 64, two V^T 64.
+// after phase 2); the two S, K and V register sets alternate between
+// consecutive steps (the loop is unrolled by 2).  Half blocks keep the live
+// set at about 470 registers: O^T 128, two S 64, P 16, Q 64 (in AGPRs, read
+// there by the MFMAs), two K 64, two V^T 64.
 // With SB (head_dim 256) K / V^T keep one set each: K(u+2) requested after
 // phase 1 and V^T(u+1) after phase 2, each a phase ahead of use; phase 1
 // forms the second half of P(u) beside the S(u+1) MFMAs, and phase 2 forms
 // the lane maxima of S(u+1), tests them against the lazy threshold and then
-// forms the first half of P(u+1) (the rescale follows phase 2 when an
-// offset moved).  Head_dim 256 (QLDS) doubles
-// O^T, K and V^T, so Q moves to LDS and O^T (256 registers for 64 rows) to
-// the AGPR file (OA), where only the P.V MFMAs touch it.
+// forms the first half of P(u+1) (the rescale follows phase 2 when an offset
+// moved).  Head_dim 256 (QLDS) doubles O^T, K and V^T, so Q moves to LDS and
+// O^T (256 registers for 64 rows) to the AGPR file (OA), where only the P.V
+// MFMAs touch it.
 // The tile's kv_idx row is compacted into LDS once (visited blocks only), so
 // sentinel and invisible slots cost nothing in the loop.
 // Per-wave LDS bytes of attn_fwd_pipe_kernel: Q fragments (QLDS), block
