@@ -676,12 +676,13 @@ __global__ __launch_bounds__(64 * (4 / NT)) void attn_fwd_pipe_kernel(
     }
     mask(nxt, uni(rm1), (u + 1) & 1, mbits(u + 1));
     // K(u+3) into kc (free once phase 1 has read K(u+1)): one slab every
-    // second MFMA pair of phase 2 rather than all eight at once, so the four
-    // waves of a CU do not load in bursts (c2 / c3 / c4 attention 1.0-1.4 %
-    // faster than the burst after phase 1, same box)
+    // second MFMA pair of phase 2 (the odd ones) rather than all eight at
+    // once, so the four waves of a CU do not load in bursts (c2 / c3 / c4
+    // attention 1.0-1.4 % faster than the burst after phase 1, same box;
+    // odd pairs 0.3 % faster than even ones)
     static_assert(P2 >= 4 * KS, "every K slab is requested within phase 2");
     phase2s(nxt, vc, [&](int j) {
-      if ((j & 1) == 0 && j / 2 < 2 * KS) kc[(j / 2) / KS][(j / 2) % KS] = slab(kp, j / 2);
+      if ((j & 1) == 1 && j / 2 < 2 * KS) kc[(j / 2) / KS][(j / 2) % KS] = slab(kp, j / 2);
     });
     load_v(uni(rv), clamp_u(u + 2) & 1, vc);
   };
