@@ -22,10 +22,10 @@ namespace ugbsa {
 // V^T operands are prefetched into registers two half blocks ahead (K(u+3)
 // is requested during phase 2, one 1 KiB slab per two MFMA pairs, V^T(u+2)
 // two fragments at a time as the last row set's P.V MFMAs free them); the
-// two S, K and V register sets alternate between
-// consecutive steps (the loop is unrolled by 2).  Half blocks keep the live
-// set at about 470 registers: O^T 128, two S 64, P 16, Q 64 (in AGPRs, read
-// there by the MFMAs), two K 64, two V^T 64.
+// two S, K and V register sets alternate between consecutive steps (the loop
+// is unrolled by 2).  Half blocks keep the live set at about 470 registers:
+// O^T 128, two S 64, P 16, Q 64 (in AGPRs, read there by the MFMAs), two K
+// 64, two V^T 64.
 // With SB (head_dim 256) K / V^T keep one set each: K(u+2) requested after
 // phase 1 and V^T(u+1) after phase 2, each a phase ahead of use; phase 1
 // forms the second half of P(u) beside the S(u+1) MFMAs, and phase 2 forms
